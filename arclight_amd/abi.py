@@ -1,0 +1,105 @@
+"""ctypes mirror of include/arclight_fattn.h (structures and constants only).
+
+Loading no library, this module is shared by the product binding
+(arclight_amd._lib) and by the CPU oracle's binding, which implement the same
+operator interface: ArcLight's NNML_OP_FLASH_ATTN_EXT node with src tensors
+q, k, v, mask, sinks and op_params {scale, max_bias, logit_softcap, prec}
+(nnml/src/tensor.cpp:1292-1338, nnml/src/ops/ops.cpp:1432-1445).
+"""
+import ctypes
+
+AL_TYPE_F32 = 0
+AL_TYPE_F16 = 1
+AL_TYPE_I32 = 26
+AL_TYPE_I64 = 27
+
+AL_PREC_DEFAULT = 0
+AL_PREC_F32 = 10
+
+AL_OK = 0
+AL_ERR_INVALID = -1
+AL_ERR_UNSUPPORTED = -2
+AL_ERR_HIP = -3
+AL_ERR_WORKSPACE = -4
+
+STATUS_NAMES = {
+    AL_OK: "AL_OK",
+    AL_ERR_INVALID: "AL_ERR_INVALID",
+    AL_ERR_UNSUPPORTED: "AL_ERR_UNSUPPORTED",
+    AL_ERR_HIP: "AL_ERR_HIP",
+    AL_ERR_WORKSPACE: "AL_ERR_WORKSPACE",
+}
+
+TYPE_SIZES = {AL_TYPE_F32: 4, AL_TYPE_F16: 2, AL_TYPE_I32: 4, AL_TYPE_I64: 8}
+
+
+class AlTensor(ctypes.Structure):
+    _fields_ = [
+        ("data", ctypes.c_void_p),
+        ("type", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("ne", ctypes.c_int64 * 4),
+        ("nb", ctypes.c_uint64 * 4),
+    ]
+
+
+class AlFattnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", AlTensor),
+        ("k", AlTensor),
+        ("v", AlTensor),
+        ("mask", AlTensor),
+        ("sinks", AlTensor),
+        ("dst", AlTensor),
+        ("scale", ctypes.c_float),
+        ("max_bias", ctypes.c_float),
+        ("logit_softcap", ctypes.c_float),
+        ("prec", ctypes.c_int32),
+        ("kv_len", ctypes.c_int64),
+        ("causal_pos0", ctypes.c_int64),
+        ("stream", ctypes.c_void_p),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
+    ]
+
+
+def make_tensor(data, typ, ne, nb=None):
+    """Builds an AlTensor. `ne` is nnml order (ne[0] fastest); `nb` defaults to
+    contiguous byte strides."""
+    t = AlTensor()
+    t.data = data if data else None
+    t.type = typ
+    ne = list(ne) + [1] * (4 - len(ne))
+    if nb is None:
+        nb = [TYPE_SIZES[typ]]
+        for i in range(1, 4):
+            nb.append(nb[i - 1] * ne[i - 1])
+    for i in range(4):
+        t.ne[i] = int(ne[i])
+        t.nb[i] = int(nb[i])
+    return t
+
+
+def empty_tensor():
+    return make_tensor(None, AL_TYPE_F32, [0, 0, 0, 0], [0, 0, 0, 0])
+
+
+# Physical numpy layouts of each operand, as the axis of the numpy array that
+# holds nnml dim ne0..ne3. These are the layouts the Qwen3 graph produces
+# (nnml/src/cgraph.cpp:250-258, 1072-1102; store at arm.cpp:2431):
+#   q     array (B, T, Hq, D)        f32  -> ne = [D, T, Hq, B]
+#   k, v  array (B, n_kv, Hkv, D)    f16  -> ne = [D, n_kv, Hkv, B]
+#   mask  array (m3, m2, rows, n_kv) f16  -> ne = [n_kv, rows, m2, m3]
+#   dst   array (B, T, Hq, D)        f32  -> ne = [D, Hq, T, B]
+Q_AXES = (3, 1, 2, 0)
+KV_AXES = (3, 1, 2, 0)
+MASK_AXES = (3, 2, 1, 0)
+DST_AXES = (3, 2, 1, 0)
+
+
+def tensor_desc(data, typ, shape, strides, axes):
+    """AlTensor for an array of numpy `shape`/`strides` (bytes) whose nnml dim
+    i lives on numpy axis axes[i]."""
+    ne = [int(shape[a]) for a in axes]
+    nb = [int(strides[a]) for a in axes]
+    return make_tensor(data, typ, ne, nb)

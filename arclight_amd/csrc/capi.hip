@@ -1,0 +1,310 @@
+// Host side of the C ABI: operand validation (the reference's asserts),
+// kernel selection, split-KV sizing, workspace management and launch.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/arclight_fattn.h"
+#include "fattn_kernels.hpp"
+#include "kv_write.hpp"
+#include "runtime.hpp"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+}  // namespace
+
+int al_fail(int code, const char * fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int al_hip_fail(hipError_t e, const char * what) {
+    return al_fail(AL_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+void al_clear_error() { g_last_error.clear(); }
+
+// ---------------------------------------------------------------------------
+// per-device state
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct DeviceState {
+    bool       init = false;
+    int        n_cu = 0;
+    void *     ws = nullptr;        // library-owned split-KV workspace
+    size_t     ws_bytes = 0;
+    int *      err = nullptr;       // kernel-recorded errors (set_rows)
+};
+
+std::mutex g_mu;
+std::vector<DeviceState> g_dev;
+
+}  // namespace
+
+static int device_state(int * dev_out, DeviceState ** st_out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return al_hip_fail(e, "hipGetDevice");
+    std::lock_guard<std::mutex> lk(g_mu);
+    if ((int) g_dev.size() <= dev) g_dev.resize(dev + 1);
+    DeviceState & st = g_dev[dev];
+    if (!st.init) {
+        e = hipDeviceGetAttribute(&st.n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return al_hip_fail(e, "hipDeviceGetAttribute");
+        e = hipMalloc((void **) &st.err, 256);
+        if (e != hipSuccess) return al_hip_fail(e, "hipMalloc(error flag)");
+        e = hipMemset(st.err, 0, 256);
+        if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
+        st.init = true;
+    }
+    *dev_out = dev;
+    *st_out = &st;
+    return AL_OK;
+}
+
+int al_device_error_flag(int ** flag) {
+    int dev;
+    DeviceState * st;
+    const int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    *flag = st->err;
+    return AL_OK;
+}
+
+int al_device_cu_count(int * n_cu) {
+    int dev;
+    DeviceState * st;
+    const int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    *n_cu = st->n_cu;
+    return AL_OK;
+}
+
+// Library-owned workspace, zero-filled when (re)allocated. The kernels leave
+// the counter region zeroed after every call.
+static int library_workspace(size_t bytes, void ** ptr) {
+    int dev;
+    DeviceState * st;
+    const int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (st->ws_bytes < bytes) {
+        if (st->ws) {
+            hipError_t e = hipDeviceSynchronize();
+            if (e != hipSuccess) return al_hip_fail(e, "hipDeviceSynchronize");
+            e = hipFree(st->ws);
+            if (e != hipSuccess) return al_hip_fail(e, "hipFree(workspace)");
+            st->ws = nullptr;
+            st->ws_bytes = 0;
+        }
+        const size_t sz = std::max(bytes, (size_t) 4 << 20);
+        hipError_t e = hipMalloc(&st->ws, sz);
+        if (e != hipSuccess) return al_fail(AL_ERR_HIP, "hipMalloc(workspace %zu bytes): %s", sz, hipGetErrorString(e));
+        e = hipMemset(st->ws, 0, sz);
+        if (e != hipSuccess) return al_hip_fail(e, "hipMemset(workspace)");
+        st->ws_bytes = sz;
+    }
+    *ptr = st->ws;
+    return AL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// flash attention
+// ---------------------------------------------------------------------------
+
+namespace {
+
+struct Plan {
+    FattnParams p;
+    int rows_per_tile = 16;
+    size_t counters_bytes = 0;
+    size_t part_bytes = 0;
+};
+
+bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
+
+int wgs_per_cu() {
+    static int v = [] {
+        const char * s = getenv("AL_SPLITKV_WGS_PER_CU");
+        const int x = s ? atoi(s) : 0;
+        return x > 0 ? x : 2;
+    }();
+    return v;
+}
+
+// Mirrors the asserts of nnml_flash_attn_ext (nnml/src/tensor.cpp:1292-1320)
+// and nnml_compute_forward_flash_attn_ext_f16 (arm.cpp:2213-2245), then the
+// limits of this path.
+int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
+    if (!a) return al_fail(AL_ERR_INVALID, "fattn: null arguments");
+    const al_tensor &q = a->q, &k = a->k, &v = a->v, &m = a->mask, &s = a->sinks, &d = a->dst;
+    if (!q.data || !k.data || !v.data || !d.data) return al_fail(AL_ERR_INVALID, "fattn: q, k, v and dst are required");
+    if (a->prec != AL_PREC_DEFAULT && a->prec != AL_PREC_F32)
+        return al_fail(AL_ERR_INVALID, "fattn: prec %d is not DEFAULT or F32 (ops.cpp:1441-1443)", a->prec);
+    const int64_t D = k.ne[0], DV = v.ne[0], T = q.ne[1], Hq = q.ne[2], B = q.ne[3];
+    const int64_t n_kv = k.ne[1], Hkv = k.ne[2];
+    // nnml_can_mul_mat(k, q) (tensor.cpp:1294)
+    if (q.ne[0] != D) return al_fail(AL_ERR_INVALID, "fattn: q ne0 %lld != k ne0 %lld", (long long) q.ne[0], (long long) D);
+    if (Hkv <= 0 || Hq % Hkv != 0 || k.ne[3] <= 0 || B % k.ne[3] != 0)
+        return al_fail(AL_ERR_INVALID, "fattn: q heads/streams (%lld, %lld) do not broadcast over k (%lld, %lld)",
+                       (long long) Hq, (long long) B, (long long) Hkv, (long long) k.ne[3]);
+    if (v.ne[1] != n_kv) return al_fail(AL_ERR_INVALID, "fattn: v cells %lld != k cells %lld", (long long) v.ne[1], (long long) n_kv);
+    if (v.ne[2] <= 0 || Hq % v.ne[2] != 0 || v.ne[3] <= 0 || B % v.ne[3] != 0)
+        return al_fail(AL_ERR_INVALID, "fattn: q heads/streams do not broadcast over v");
+    // rows contiguous (arm.cpp:2224-2226)
+    if (q.nb[0] != 4 || k.nb[0] != 2 || v.nb[0] != 2) return al_fail(AL_ERR_INVALID, "fattn: q/k/v rows must be contiguous");
+    // dst not permuted (arm.cpp:2219-2238)
+    if (d.ne[0] != DV || d.ne[1] != Hq || d.ne[2] != T || d.ne[3] != B)
+        return al_fail(AL_ERR_INVALID, "fattn: dst must be [DV, Hq, T, B]");
+    if (d.nb[0] != 4 || d.nb[0] > d.nb[1] || d.nb[1] > d.nb[2] || d.nb[2] > d.nb[3])
+        return al_fail(AL_ERR_INVALID, "fattn: dst cannot be transposed or permuted");
+    if (m.data) {
+        const int64_t tpad = (T + 63) / 64 * 64;
+        if (m.ne[1] < tpad) return al_fail(AL_ERR_INVALID, "fattn: mask has %lld rows, needs >= PAD(T,64) = %lld (tensor.cpp:1300-1301)",
+                                           (long long) m.ne[1], (long long) tpad);
+        if (m.ne[0] < n_kv) return al_fail(AL_ERR_INVALID, "fattn: mask has %lld columns < n_kv %lld", (long long) m.ne[0], (long long) n_kv);
+        if (m.ne[2] <= 0 || m.ne[3] <= 0 || Hq % m.ne[2] != 0 || B % m.ne[3] != 0)
+            return al_fail(AL_ERR_INVALID, "fattn: mask dims 2/3 do not broadcast (tensor.cpp:1302-1303)");
+        if (m.nb[0] != 2) return al_fail(AL_ERR_INVALID, "fattn: mask must be contiguous (tensor.cpp:1298)");
+    } else if (a->max_bias > 0.0f) {
+        return al_fail(AL_ERR_INVALID, "fattn: max_bias > 0 requires a mask (tensor.cpp:1305-1307)");
+    }
+    if (s.data && (s.type != AL_TYPE_F32 || s.ne[0] != Hq))
+        return al_fail(AL_ERR_INVALID, "fattn: sinks must be f32 [Hq] (tensor.cpp:1328-1329)");
+
+    // limits of this path
+    if (q.type != AL_TYPE_F32) return al_fail(AL_ERR_UNSUPPORTED, "fattn: q type %d (f32 only)", q.type);
+    if (k.type != AL_TYPE_F16 || v.type != AL_TYPE_F16)
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn: k/v types %d/%d (f16 K/V cache only)", k.type, v.type);
+    if (d.type != AL_TYPE_F32) return al_fail(AL_ERR_UNSUPPORTED, "fattn: dst type %d (f32 only)", d.type);
+    if (m.data && m.type != AL_TYPE_F16) return al_fail(AL_ERR_UNSUPPORTED, "fattn: mask type %d (f16 only)", m.type);
+    if (D != 128 || DV != 128) return al_fail(AL_ERR_UNSUPPORTED, "fattn: head dim %lld/%lld (128 only)", (long long) D, (long long) DV);
+    if (v.ne[2] != Hkv || v.ne[3] != k.ne[3]) return al_fail(AL_ERR_UNSUPPORTED, "fattn: k and v must have the same heads and streams");
+    if (!aligned16(q.data) || !aligned16(k.data) || !aligned16(v.data) || !aligned16(d.data) ||
+        q.nb[1] % 16 || q.nb[2] % 16 || q.nb[3] % 16 || k.nb[1] % 16 || k.nb[2] % 16 || k.nb[3] % 16 ||
+        v.nb[1] % 16 || v.nb[2] % 16 || v.nb[3] % 16 || d.nb[1] % 16)
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn: operands must be 16-byte aligned with 16-byte multiple strides");
+    if (n_kv <= 0 || n_kv > INT32_MAX / 2 || T <= 0 || T > (1 << 24) || B > 65535 || Hq * T > INT32_MAX / 2)
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn: sizes out of range");
+
+    Plan pl;
+    FattnParams & p = pl.p;
+    memset(&p, 0, sizeof(p));
+    p.q = (const char *) q.data; p.q_nb1 = q.nb[1]; p.q_nb2 = q.nb[2]; p.q_nb3 = q.nb[3];
+    p.k = (const char *) k.data; p.k_nb1 = k.nb[1]; p.k_nb2 = k.nb[2]; p.k_nb3 = k.nb[3];
+    p.v = (const char *) v.data; p.v_nb1 = v.nb[1]; p.v_nb2 = v.nb[2]; p.v_nb3 = v.nb[3];
+    if (m.data) {
+        p.mask = (const char *) m.data; p.m_nb1 = m.nb[1]; p.m_nb2 = m.nb[2]; p.m_nb3 = m.nb[3];
+        p.m_ne0 = (int32_t) std::min<int64_t>(m.ne[0], INT32_MAX); p.m_ne2 = (int32_t) m.ne[2]; p.m_ne3 = (int32_t) m.ne[3];
+    }
+    p.sinks = (const float *) s.data;
+    p.dst = (char *) d.data; p.dst_nb1 = d.nb[1];
+    p.T = (int32_t) T; p.Hq = (int32_t) Hq; p.Hkv = (int32_t) Hkv; p.G = (int32_t) (Hq / Hkv); p.B = (int32_t) B;
+    p.R = p.T * p.G;
+    p.rk3 = (int32_t) (B / k.ne[3]); p.rv3 = (int32_t) (B / v.ne[3]);
+    p.n_kv = (int32_t) n_kv;
+    p.kv_hi = (int32_t) ((a->kv_len <= 0 || a->kv_len > n_kv) ? n_kv : a->kv_len);
+    p.causal_pos0 = a->causal_pos0 < 0 ? -1 : a->causal_pos0;
+    p.softcap = a->logit_softcap;
+    p.scale = a->scale;
+    if (p.softcap != 0.0f) p.scale /= p.softcap;                        // arm.cpp:2267-2269
+    p.max_bias = a->max_bias;
+    p.n_head_log2 = 1u << (uint32_t) floor(log2((double) Hq));          // arm.cpp:2271-2274
+    p.m0 = powf(2.0f, -(p.max_bias) / p.n_head_log2);
+    p.m1 = powf(2.0f, -(p.max_bias / 2.0f) / p.n_head_log2);
+
+    // split-KV sizing
+    pl.rows_per_tile = fattn_splitkv_rows_per_tile(std::min(p.R, 64));
+    p.n_row_tiles = (p.R + pl.rows_per_tile - 1) / pl.rows_per_tile;
+    int64_t extent = p.kv_hi;
+    if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
+    extent = std::max<int64_t>(extent, 0);
+    const int64_t tiles = (extent + 31) / 32;
+    const int64_t units = (int64_t) Hkv * p.n_row_tiles * B;
+    const int64_t target = (int64_t) n_cu * wgs_per_cu();
+    int64_t n_split = (target + units - 1) / units;
+    n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, (tiles + 3) / 4));
+    int64_t cps_tiles = (tiles + n_split - 1) / n_split;
+    cps_tiles = std::max<int64_t>(cps_tiles, 1);
+    p.cells_per_split = (int32_t) (cps_tiles * 32);
+    n_split = std::max<int64_t>(1, (extent + p.cells_per_split - 1) / p.cells_per_split);
+    p.n_split = (int32_t) n_split;
+    if (p.n_split > 1) {
+        pl.counters_bytes = ((size_t) units * sizeof(unsigned) + 255) & ~(size_t) 255;
+        pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
+    }
+    *out = pl;
+    return AL_OK;
+}
+
+}  // namespace
+
+extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
+    int n_cu = 0;
+    if (al_device_cu_count(&n_cu) != AL_OK) return 0;
+    Plan pl;
+    if (make_plan(a, n_cu, &pl) != AL_OK) return 0;
+    return pl.counters_bytes + pl.part_bytes;
+}
+
+extern "C" int al_fattn_f16(const al_fattn_args * a) {
+    int n_cu = 0;
+    int rc = al_device_cu_count(&n_cu);
+    if (rc != AL_OK) return rc;
+    Plan pl;
+    rc = make_plan(a, n_cu, &pl);
+    if (rc != AL_OK) return rc;
+    const size_t need = pl.counters_bytes + pl.part_bytes;
+    if (need) {
+        void * ws = a->workspace;
+        if (ws) {
+            if (a->workspace_bytes < need)
+                return al_fail(AL_ERR_WORKSPACE, "fattn: workspace %llu bytes < %zu needed",
+                               (unsigned long long) a->workspace_bytes, need);
+        } else {
+            rc = library_workspace(need, &ws);
+            if (rc != AL_OK) return rc;
+        }
+        pl.p.counters = (unsigned *) ws;
+        pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
+    }
+    const hipError_t e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream);
+    if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
+    return AL_OK;
+}
+
+extern "C" const char * al_last_error(void) { return g_last_error.c_str(); }
+
+extern "C" const char * al_version(void) { return "arclight_amd fattn 0.1 (gfx950)"; }
+
+extern "C" int al_device_errors(void) {
+    int * flag = nullptr;
+    int rc = al_device_error_flag(&flag);
+    if (rc != AL_OK) return rc;
+    int h[2] = {0, 0};
+    hipError_t e = hipMemcpy(h, flag, sizeof(h), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return al_hip_fail(e, "hipMemcpy(error flag)");
+    if (h[0]) {
+        e = hipMemset(flag, 0, sizeof(h));
+        if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
+        return al_fail(AL_ERR_INVALID, "set_rows: row index %d out of range (ops.cpp:171)", h[1]);
+    }
+    return AL_OK;
+}

@@ -1,0 +1,50 @@
+// Device-side building blocks shared by the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define AL_INF __builtin_inff()
+
+// D[16x16] += A[16x32] * B[32x16], f16 inputs, f32 accumulation (gfx950).
+// Lane l = 16*g + n holds A row n, B column n, k-slots 8g..8g+7 of each,
+// and D rows 4g..4g+3 of column n.
+__device__ __forceinline__ floatx4 mfma_16x16x32(half8 a, half8 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// e^x through the hardware exp2 (v_exp_f32).
+__device__ __forceinline__ float exp_fast(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
+__device__ __forceinline__ half8 as_half8(u32x4 v) { return __builtin_bit_cast(half8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(uint4 v) { u32x4 r = {v.x, v.y, v.z, v.w}; return r; }
+
+// 8 f32 -> 8 f16, IEEE round-to-nearest-even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ half8 to_half8(float4 a, float4 b) {
+    half8 h;
+    h[0] = (_Float16) a.x; h[1] = (_Float16) a.y; h[2] = (_Float16) a.z; h[3] = (_Float16) a.w;
+    h[4] = (_Float16) b.x; h[5] = (_Float16) b.y; h[6] = (_Float16) b.z; h[7] = (_Float16) b.w;
+    return h;
+}
+
+__device__ __forceinline__ float f16_bits_to_float(uint16_t b) {
+    return (float) __builtin_bit_cast(_Float16, b);
+}
+
+// max / sum over the 4 lanes {n, n+16, n+32, n+48} that share column n.
+__device__ __forceinline__ float colmax4(float x) {
+    x = fmaxf(x, __shfl_xor(x, 16));
+    x = fmaxf(x, __shfl_xor(x, 32));
+    return x;
+}
+__device__ __forceinline__ float colsum4(float x) {
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}

@@ -1,0 +1,40 @@
+// Kernel-side parameter block and launchers of the attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+// Everything a flash-attention kernel needs, resolved on the host from the
+// al_fattn_args descriptors. Byte strides; pointers are device pointers.
+struct FattnParams {
+    const char * q;     int64_t q_nb1, q_nb2, q_nb3;     // f32 [D, T, Hq, B]
+    const char * k;     int64_t k_nb1, k_nb2, k_nb3;     // f16 [D, n_kv, Hkv, Bk]
+    const char * v;     int64_t v_nb1, v_nb2, v_nb3;     // f16 [D, n_kv, Hkv, Bv]
+    const char * mask;  int64_t m_nb1, m_nb2, m_nb3;     // f16 [m_ne0, rows, m_ne2, m_ne3] or null
+    int32_t m_ne0, m_ne2, m_ne3;
+    const float * sinks;                                 // f32 [Hq] or null
+    char * dst;         int64_t dst_nb1;                 // f32 rows (i3*T + i1)*Hq + i2
+
+    int32_t T, Hq, Hkv, G, B, R;    // R = T*G query rows per kv head
+    int32_t rk3, rv3;               // q streams per k / v stream
+    int32_t n_kv;                   // cells addressable in k/v
+    int32_t kv_hi;                  // cells >= kv_hi are masked for all rows
+    int64_t causal_pos0;            // < 0: off
+    float   scale;                  // already divided by softcap when softcap != 0
+    float   softcap;
+    float   max_bias, m0, m1;
+    uint32_t n_head_log2;
+
+    int32_t n_row_tiles;
+    int32_t n_split;
+    int32_t cells_per_split;        // multiple of 32
+    float *    part;                // split-KV merge records
+    unsigned * counters;            // one per (stream, kv head, row tile), zero between calls
+};
+
+// Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).
+int fattn_splitkv_rows_per_tile(int R);
+hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
+
+// Floats of one split-KV merge record row (O[128], m, l, pad).
+constexpr int kFattnRecordStride = 132;

@@ -1,0 +1,159 @@
+/*
+ * arclight_fattn.h - C ABI of the MI355X (gfx950) flash-attention operator.
+ *
+ * This is the drop-in boundary for ArcLight's NNML_OP_FLASH_ATTN_EXT. The
+ * reference executes that op as
+ *     void nnml_compute_forward_flash_attn_ext(nnml_tensor * node,
+ *                                              const nnml_compute_state * params)
+ * (nnml/include/ops.h:433, nnml/src/ops/ops.cpp:1432-1445), which reads its
+ * operands as node->get_src_tensor(0..4) = q, k, v, mask, sinks
+ * (nnml/src/ops/arm/arm.cpp:2197-2202, nnml/src/tensor.cpp:1314-1318,1331),
+ * its parameters from op_params f32[0..2] = {scale, max_bias, logit_softcap}
+ * and i32[3] = prec (tensor.cpp:1311, 1334-1338), and writes node->data.
+ *
+ * Here every operand travels as an al_tensor: a data pointer plus nnml's
+ * ne[4] element counts and nb[4] byte strides, with nnml's type numbering.
+ * All data pointers are DEVICE pointers (HBM). No pointer is retained after
+ * a call returns; the caller owns every buffer.
+ *
+ * Operand layouts are the ones the Qwen3 graph hands to the op
+ * (nnml/src/cgraph.cpp:245-294, 1057-1112):
+ *   q     f32  ne = [D,  T,    Hq,  B ]   (token, head, stream strides nb1..nb3)
+ *   k     f16  ne = [D,  n_kv, Hkv, B ]   (cell-major cache view: nb1 = Hkv*D*2)
+ *   v     f16  ne = [D,  n_kv, Hkv, B ]
+ *   mask  f16  ne = [n_kv, >= PAD(T,64), m2, m3]   (0 / -inf, optional)
+ *   sinks f32  ne = [Hq]                            (optional)
+ *   dst   f32  ne = [D,  Hq,   T,   B ]   row of (i3, i1, i2) at
+ *              (i3*T*Hq + i1*Hq + i2) * nb1           (arm.cpp:2431)
+ *
+ * Error convention: every entry point returns AL_OK (0) or a negative
+ * status; al_last_error() gives the message of the calling thread's last
+ * failure. The reference aborts on the same preconditions (NNML_ASSERT,
+ * nnml/include/nnml.h:97-111); an nnml-side shim turns a non-zero status into
+ * NNML_ABORT.
+ */
+#ifndef ARCLIGHT_FATTN_H
+#define ARCLIGHT_FATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types, numbered as enum nnml_type (nnml/include/ops.h:140-171). */
+enum {
+    AL_TYPE_F32 = 0,
+    AL_TYPE_F16 = 1,
+    AL_TYPE_I32 = 26,
+    AL_TYPE_I64 = 27
+};
+
+/* Accumulation precision, as enum nnml_prec (nnml/include/ops.h:174-177). */
+enum {
+    AL_PREC_DEFAULT = 0,
+    AL_PREC_F32     = 10
+};
+
+/* Status codes. */
+enum {
+    AL_OK              = 0,
+    AL_ERR_INVALID     = -1,  /* precondition the reference asserts        */
+    AL_ERR_UNSUPPORTED = -2,  /* valid for the reference, not on this path */
+    AL_ERR_HIP         = -3,  /* HIP runtime error                         */
+    AL_ERR_WORKSPACE   = -4   /* caller workspace too small                */
+};
+
+/* One operand: nnml_tensor's data/type/ne/nb (nnml/include/tensor.h:78-198). */
+typedef struct al_tensor {
+    void *   data;
+    int32_t  type;
+    int32_t  reserved;
+    int64_t  ne[4];
+    uint64_t nb[4];
+} al_tensor;
+
+/*
+ * Arguments of one flash-attention call.
+ *
+ * q, k, v, dst are required. mask.data == NULL means "no mask" and
+ * sinks.data == NULL means "no sinks", as a NULL src tensor does in the
+ * reference (arm.cpp:2226-2231, 2402).
+ *
+ * kv_len and causal_pos0 describe masking without a mask tensor, and act as
+ * hints when a mask is also given:
+ *   - cells c >= kv_len are masked for every query row (kv_len <= 0: n_kv);
+ *   - when causal_pos0 >= 0, cell c is masked for query token t when
+ *     c > causal_pos0 + t.
+ * With a mask tensor present these must agree with it (the nnml shim derives
+ * them from the mask it stages); the result is then identical to the
+ * explicit mask alone, while wholly masked tiles are skipped unread.
+ *
+ * workspace: device scratch for split-KV partials. NULL lets the library use
+ * its own per-device buffer (allocated on first use, grown when needed).
+ * Calls that share one workspace must be ordered on one stream.
+ */
+typedef struct al_fattn_args {
+    al_tensor q;
+    al_tensor k;
+    al_tensor v;
+    al_tensor mask;
+    al_tensor sinks;
+    al_tensor dst;
+    float     scale;          /* op_params f32[0] */
+    float     max_bias;       /* op_params f32[1] (ALiBi)   */
+    float     logit_softcap;  /* op_params f32[2]           */
+    int32_t   prec;           /* op_params i32[3]           */
+    int64_t   kv_len;
+    int64_t   causal_pos0;
+    void *    stream;         /* hipStream_t; NULL = default stream */
+    void *    workspace;
+    uint64_t  workspace_bytes;
+} al_fattn_args;
+
+/*
+ * Flash attention, f16 K/V, f32 Q and output, f32 accumulation.
+ * Replaces nnml_compute_forward_flash_attn_ext (nnml/src/ops/ops.cpp:1432-1445)
+ * -> nnml_compute_forward_flash_attn_ext_f16 (nnml/src/ops/arm/arm.cpp:2196-2433).
+ * Enqueues on args->stream and returns without synchronizing.
+ */
+int al_fattn_f16(const al_fattn_args * args);
+
+/* Workspace bytes al_fattn_f16 needs for these arguments (0 if none). */
+uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
+
+/* Message of the calling thread's most recent failure ("" if none). */
+const char * al_last_error(void);
+
+/*
+ * KV write: dst[idx[i]] = f16(src[i]) row by row, IEEE round-to-nearest-even.
+ * Replaces nnml_compute_forward_set_rows (nnml/src/ops/ops.cpp:1300-1320) ->
+ * nnml_compute_forward_set_rows_f32 (ops.cpp:135-181) for an f16 destination,
+ * the op llm_kv_cache::cpy_k / cpy_v build (nnml/src/cgraph.cpp:1114-1180).
+ *   dst f16 ne = [nc, n_rows_dst, d2, d3]   (the cache, device)
+ *   src f32 ne = [nc, n_rows,     d2, d3]
+ *   idx i64 or i32 ne = [n_rows, i1, i2]  (broadcast over d2 % i1, d3 % i2)
+ * Enqueues on `stream` without synchronizing. A row whose index lies outside
+ * [0, n_rows_dst) is not written; the kernel records it, and the next
+ * al_device_errors() after the stream completes returns AL_ERR_INVALID
+ * (the reference asserts on it, ops.cpp:171).
+ */
+int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
+                        const al_tensor * idx, void * stream);
+
+/*
+ * Reports and clears errors that kernels recorded on the current device
+ * (out-of-range set_rows indices). Call after synchronizing the stream.
+ * Returns AL_OK or AL_ERR_INVALID with al_last_error() set.
+ */
+int al_device_errors(void);
+
+/* Library version string. */
+const char * al_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ARCLIGHT_FATTN_H */

@@ -1,0 +1,405 @@
+/*
+ * fattn_oracle.c - CPU oracle for ArcLight's flash-attention op.
+ *
+ * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+ * Nothing in the product path links or calls this file.
+ *
+ * Restated from (paths relative to the ArcLight tree):
+ *   nnml/src/ops/arm/arm.cpp:2196-2433  nnml_compute_forward_flash_attn_ext_f16
+ *   nnml/src/ops/arm/arm.cpp:286-386    nnml_vec_dot_f16 (O3 lane structure)
+ *   nnml/src/ops/arm/arm.cpp:1453-1755  vec_scale / vec_mad f16 and f32
+ *   nnml/src/ops/arm/common.cpp:11-24   f32 -> f16 row conversion
+ *   nnml/include/ops.h:276-323          IEEE fp16 conversions (RNE)
+ *   nnml/src/ops/ops.cpp:135-181        set_rows f32 -> f16
+ *   nnml/src/tensor.cpp:1292-1338       operand preconditions
+ *
+ * Pinning (tests/test_oracle_*.py): the fp16 conversions are compared bit
+ * for bit with numpy's IEEE conversions over every f16 pattern and millions
+ * of f32 patterns; O1 is compared with scipy.special.softmax attention; O2
+ * with O1; all three with closed forms (single visible cell, equal scores,
+ * dominant score, masked cells, all-masked rows, sinks, softcap, ALiBi slopes
+ * from the ALiBi paper's construction), permutation invariance and
+ * chunked-equals-one-shot causal prefill.
+ */
+#include "fattn_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* fp16 <-> fp32, IEEE binary16, round to nearest even                 */
+/* ------------------------------------------------------------------ */
+
+static inline uint32_t f32_bits(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float bits_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t orc_f32_to_f16(float f) {
+    const uint32_t x    = f32_bits(f);
+    const uint16_t sign = (uint16_t) ((x >> 16) & 0x8000u);
+    const uint32_t ax   = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) {           /* NaN: quiet NaN, as ops.h:322 */
+        return sign | 0x7e00u;
+    }
+    if (ax >= 0x477ff000u) {          /* >= 65520 rounds to infinity */
+        return sign | 0x7c00u;
+    }
+    const uint32_t e = ax >> 23;      /* biased f32 exponent */
+    if (e < 113) {                    /* below 2^-14: f16 subnormal or zero */
+        if (e < 102) {                /* below 2^-25: rounds to zero */
+            return sign;
+        }
+        const uint32_t m     = (ax & 0x7fffffu) | 0x800000u;
+        const uint32_t shift = 126 - e;          /* 14..24 */
+        uint32_t q           = m >> shift;
+        const uint32_t rem   = m & ((1u << shift) - 1u);
+        const uint32_t half  = 1u << (shift - 1);
+        if (rem > half || (rem == half && (q & 1u))) {
+            q++;
+        }
+        return sign | (uint16_t) q;   /* q == 0x400 is the smallest normal */
+    }
+    uint32_t h         = ((e - 112) << 10) | ((ax & 0x7fffffu) >> 13);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) {
+        h++;                          /* a carry rolls into the exponent */
+    }
+    return sign | (uint16_t) h;
+}
+
+float orc_f16_to_f32(uint16_t h) {
+    const uint32_t sign = ((uint32_t) h & 0x8000u) << 16;
+    const uint32_t e    = (h >> 10) & 0x1fu;
+    uint32_t m          = h & 0x3ffu;
+    if (e == 0x1f) {
+        return bits_f32(sign | 0x7f800000u | (m << 13));
+    }
+    if (e == 0) {
+        if (m == 0) {
+            return bits_f32(sign);
+        }
+        /* subnormal: m * 2^-24, exact in f32 */
+        const float v = (float) m * 0x1.0p-24f;
+        return sign ? -v : v;
+    }
+    return bits_f32(sign | ((e + 112) << 23) | (m << 13));
+}
+
+void orc_f32_to_f16_n(const float * x, uint16_t * y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f32_to_f16(x[i]);
+}
+
+void orc_f16_to_f32_n(const uint16_t * x, float * y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = orc_f16_to_f32(x[i]);
+}
+
+/* f16 arithmetic of the ARM build, emulated: one rounding to f16 per op. */
+static inline uint16_t h_fma(uint16_t acc, uint16_t a, uint16_t b) {
+    const double r = (double) orc_f16_to_f32(a) * (double) orc_f16_to_f32(b) + (double) orc_f16_to_f32(acc);
+    return orc_f32_to_f16((float) r);
+}
+static inline uint16_t h_add(uint16_t a, uint16_t b) {
+    return orc_f32_to_f16(orc_f16_to_f32(a) + orc_f16_to_f32(b));
+}
+static inline uint16_t h_mul(uint16_t a, uint16_t b) {
+    return orc_f32_to_f16(orc_f16_to_f32(a) * orc_f16_to_f32(b));
+}
+
+/* ------------------------------------------------------------------ */
+/* operand checks (tensor.cpp:1292-1320, arm.cpp:2213-2245)             */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const al_fattn_args * a;
+    int64_t D, DV, T, Hq, B, n_kv, Hkv, Bk;
+    int64_t rk2, rk3, rv2, rv3;
+    int64_t kv_len;
+    float scale, max_bias, softcap;
+    float m0, m1;
+    uint32_t n_head_log2;
+    int nth;
+    int mode;  /* 1 = O1, 2 = O2, 3 = O3 */
+} job_t;
+
+static int prepare(job_t * j, const al_fattn_args * a, int nth, int mode) {
+    memset(j, 0, sizeof(*j));
+    j->a = a;
+    j->nth = nth < 1 ? 1 : nth;
+    j->mode = mode;
+    const al_tensor *q = &a->q, *k = &a->k, *v = &a->v, *d = &a->dst;
+    if (!q->data || !k->data || !v->data || !d->data) return AL_ERR_INVALID;
+    if (q->type != AL_TYPE_F32 || k->type != AL_TYPE_F16 || v->type != AL_TYPE_F16 || d->type != AL_TYPE_F32) {
+        return AL_ERR_UNSUPPORTED;
+    }
+    j->D = k->ne[0]; j->DV = v->ne[0];
+    j->T = q->ne[1]; j->Hq = q->ne[2]; j->B = q->ne[3];
+    j->n_kv = k->ne[1]; j->Hkv = k->ne[2]; j->Bk = k->ne[3];
+    if (q->ne[0] != j->D) return AL_ERR_INVALID;
+    if (v->ne[1] != j->n_kv) return AL_ERR_INVALID;
+    if (q->nb[0] != 4 || k->nb[0] != 2 || v->nb[0] != 2) return AL_ERR_INVALID;
+    if (d->ne[0] != j->DV || d->ne[1] != j->Hq || d->ne[2] != j->T || d->ne[3] != j->B) return AL_ERR_INVALID;
+    if (d->nb[0] != 4 || d->nb[0] > d->nb[1] || d->nb[1] > d->nb[2] || d->nb[2] > d->nb[3]) return AL_ERR_INVALID;
+    if (j->Hkv <= 0 || j->Hq % j->Hkv != 0 || v->ne[2] <= 0 || j->Hq % v->ne[2] != 0) return AL_ERR_INVALID;
+    if (j->Bk <= 0 || j->B % j->Bk != 0 || v->ne[3] <= 0 || j->B % v->ne[3] != 0) return AL_ERR_INVALID;
+    j->rk2 = j->Hq / j->Hkv; j->rk3 = j->B / j->Bk;
+    j->rv2 = j->Hq / v->ne[2]; j->rv3 = j->B / v->ne[3];
+    if (a->mask.data) {
+        const al_tensor * m = &a->mask;
+        if (m->type != AL_TYPE_F16) return AL_ERR_UNSUPPORTED;
+        const int64_t tpad = (j->T + 63) / 64 * 64;
+        if (m->ne[0] < j->n_kv || m->ne[1] < tpad) return AL_ERR_INVALID;
+        if (m->ne[2] <= 0 || m->ne[3] <= 0 || j->Hq % m->ne[2] != 0 || j->B % m->ne[3] != 0) return AL_ERR_INVALID;
+        if (m->nb[0] != 2) return AL_ERR_INVALID;
+    } else if (a->max_bias > 0.0f) {
+        return AL_ERR_INVALID;  /* tensor.cpp:1305-1307 */
+    }
+    if (a->sinks.data) {
+        if (a->sinks.type != AL_TYPE_F32 || a->sinks.ne[0] != j->Hq) return AL_ERR_INVALID;
+    }
+    if (a->prec != AL_PREC_DEFAULT && a->prec != AL_PREC_F32) return AL_ERR_INVALID;  /* ops.cpp:1441-1443 */
+    j->kv_len = (a->kv_len <= 0 || a->kv_len > j->n_kv) ? j->n_kv : a->kv_len;
+
+    j->scale = a->scale;
+    j->max_bias = a->max_bias;
+    j->softcap = a->logit_softcap;
+    if (j->softcap != 0.0f) j->scale /= j->softcap;                       /* arm.cpp:2267-2269 */
+    j->n_head_log2 = 1u << (uint32_t) floor(log2((double) j->Hq));        /* arm.cpp:2271 */
+    j->m0 = powf(2.0f, -(j->max_bias) / j->n_head_log2);                   /* arm.cpp:2273 */
+    j->m1 = powf(2.0f, -(j->max_bias / 2.0f) / j->n_head_log2);            /* arm.cpp:2274 */
+    return AL_OK;
+}
+
+/* effective mask value for (token iq1, head iq2, stream iq3, cell ic) */
+static inline float mask_value(const job_t * j, const uint16_t * mp, float slope, int64_t iq1, int64_t ic) {
+    const al_fattn_args * a = j->a;
+    if (ic >= j->kv_len) return -INFINITY;
+    if (a->causal_pos0 >= 0 && ic > a->causal_pos0 + iq1) return -INFINITY;
+    return mp ? slope * orc_f16_to_f32(mp[ic]) : 0.0f;                     /* arm.cpp:2327 */
+}
+
+/* ------------------------------------------------------------------ */
+/* one query row, three numerics                                        */
+/* ------------------------------------------------------------------ */
+
+static void row_o2_o3(const job_t * j, int64_t ir, float * VKQ32, uint16_t * VKQ16, uint16_t * Q_q) {
+    const al_fattn_args * a = j->a;
+    const int64_t T = j->T, Hq = j->Hq, D = j->D, DV = j->DV;
+    const int64_t iq3 = ir / (Hq * T);                                      /* arm.cpp:2289-2291 */
+    const int64_t iq2 = (ir - iq3 * Hq * T) / T;
+    const int64_t iq1 = ir - iq3 * Hq * T - iq2 * T;
+    const uint32_t h = (uint32_t) iq2;
+    const float slope = (j->max_bias > 0.0f)
+        ? (h < j->n_head_log2 ? powf(j->m0, (float) (h + 1)) : powf(j->m1, (float) (2 * (h - j->n_head_log2) + 1)))
+        : 1.0f;                                                             /* arm.cpp:2294 */
+    float S = 0.0f;
+    float M = -INFINITY;
+    const int f16acc = (j->mode == 3);
+    if (f16acc) memset(VKQ16, 0, (size_t) DV * 2); else memset(VKQ32, 0, (size_t) DV * 4);
+
+    const uint16_t * mp = NULL;
+    if (a->mask.data) {
+        const al_tensor * m = &a->mask;
+        mp = (const uint16_t *) ((const char *) m->data + iq1 * m->nb[1] + (iq2 % m->ne[2]) * m->nb[2] + (iq3 % m->ne[3]) * m->nb[3]);
+    }
+    const int64_t ik3 = iq3 / j->rk3, ik2 = iq2 / j->rk2;
+    const int64_t iv3 = iq3 / j->rv3, iv2 = iq2 / j->rv2;
+    const float * pq = (const float *) ((const char *) a->q.data + iq1 * a->q.nb[1] + iq2 * a->q.nb[2] + iq3 * a->q.nb[3]);
+    for (int64_t d = 0; d < D; ++d) Q_q[d] = orc_f32_to_f16(pq[d]);       /* arm.cpp:2322 */
+
+    for (int64_t ic = 0; ic < j->n_kv; ++ic) {
+        const float mv = mask_value(j, mp, slope, iq1, ic);
+        if (mv == -INFINITY) continue;                                      /* arm.cpp:2328-2330 */
+        const uint16_t * kd = (const uint16_t *) ((const char *) a->k.data + ic * a->k.nb[1] + ik2 * a->k.nb[2] + ik3 * a->k.nb[3]);
+        float s;
+        if (!f16acc) {
+            /* f32 lanes of width 8, then a pairwise lane reduction */
+            float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int64_t d = 0; d < D; d += 8) {
+                for (int l = 0; l < 8 && d + l < D; ++l) acc[l] += orc_f16_to_f32(kd[d + l]) * orc_f16_to_f32(Q_q[d + l]);
+            }
+            s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
+        } else {
+            /* 4 accumulators x 8 f16 lanes, f16 FMA, f16 tree add, f32 horizontal add (arm.cpp:358-376, 89-124) */
+            uint16_t sum[4][8];
+            memset(sum, 0, sizeof(sum));
+            const int64_t np = D & ~(int64_t) 31;
+            for (int64_t i = 0; i < np; i += 32)
+                for (int jj = 0; jj < 4; ++jj)
+                    for (int l = 0; l < 8; ++l) sum[jj][l] = h_fma(sum[jj][l], kd[i + jj * 8 + l], Q_q[i + jj * 8 + l]);
+            for (int l = 0; l < 8; ++l) { sum[0][l] = h_add(sum[0][l], sum[2][l]); sum[1][l] = h_add(sum[1][l], sum[3][l]); }
+            for (int l = 0; l < 8; ++l) sum[0][l] = h_add(sum[0][l], sum[1][l]);
+            float t[4];
+            for (int l = 0; l < 4; ++l) t[l] = orc_f16_to_f32(sum[0][l]) + orc_f16_to_f32(sum[0][l + 4]);
+            double sd = (double) ((t[0] + t[1]) + (t[2] + t[3]));
+            for (int64_t i = np; i < D; ++i) sd += (double) (orc_f16_to_f32(kd[i]) * orc_f16_to_f32(Q_q[i]));
+            s = (float) sd;
+        }
+        s = s * j->scale;                                                   /* arm.cpp:2337 */
+        if (j->softcap != 0.0f) s = j->softcap * tanhf(s);                  /* arm.cpp:2339-2341 */
+        s += mv;                                                            /* arm.cpp:2343 */
+
+        const float Mold = M;
+        float ms = 1.0f, vs = 1.0f;
+        const uint16_t * vd = (const uint16_t *) ((const char *) a->v.data + ic * a->v.nb[1] + iv2 * a->v.nb[2] + iv3 * a->v.nb[3]);
+        if (s > M) {                                                        /* arm.cpp:2352-2364 */
+            M = s;
+            ms = expf(Mold - M);
+            if (f16acc) {
+                const uint16_t hs = orc_f32_to_f16(ms);
+                for (int64_t d = 0; d < DV; ++d) VKQ16[d] = h_mul(VKQ16[d], hs);
+            } else {
+                for (int64_t d = 0; d < DV; ++d) VKQ32[d] *= ms;
+            }
+        } else {
+            vs = expf(s - M);
+        }
+        if (f16acc) {
+            const uint16_t hv = orc_f32_to_f16(vs);                         /* arm.cpp:1735 */
+            for (int64_t d = 0; d < DV; ++d) VKQ16[d] = h_fma(VKQ16[d], vd[d], hv);
+        } else {
+            for (int64_t d = 0; d < DV; ++d) VKQ32[d] += orc_f16_to_f32(vd[d]) * vs;   /* arm.cpp:2385-2386 */
+        }
+        S = S * ms + vs;                                                    /* arm.cpp:2392 */
+    }
+    if (f16acc) for (int64_t d = 0; d < DV; ++d) VKQ32[d] = orc_f16_to_f32(VKQ16[d]);  /* arm.cpp:2395-2399 */
+
+    if (a->sinks.data) {                                                    /* arm.cpp:2402-2416 */
+        const float s = ((const float *) a->sinks.data)[h];
+        float ms = 1.0f, vs = 1.0f;
+        if (s > M) {
+            ms = expf(M - s);
+            for (int64_t d = 0; d < DV; ++d) VKQ32[d] *= ms;
+        } else {
+            vs = expf(s - M);
+        }
+        S = S * ms + vs;
+    }
+    const float S_inv = 1.0f / S;                                           /* arm.cpp:2419-2420 */
+    for (int64_t d = 0; d < DV; ++d) VKQ32[d] *= S_inv;
+    /* permute(0, 2, 1, 3) store (arm.cpp:2431) */
+    const int64_t ne1 = Hq, ne2 = T;
+    memcpy((char *) a->dst.data + (iq3 * ne2 * ne1 + iq2 + iq1 * ne1) * a->dst.nb[1], VKQ32, (size_t) DV * 4);
+}
+
+static void row_o1(const job_t * j, int64_t ir, double * sc, double * acc, uint16_t * Q_q) {
+    const al_fattn_args * a = j->a;
+    const int64_t T = j->T, Hq = j->Hq, D = j->D, DV = j->DV;
+    const int64_t iq3 = ir / (Hq * T);
+    const int64_t iq2 = (ir - iq3 * Hq * T) / T;
+    const int64_t iq1 = ir - iq3 * Hq * T - iq2 * T;
+    const uint32_t h = (uint32_t) iq2;
+    const double slope = (j->max_bias > 0.0f)
+        ? (h < j->n_head_log2 ? pow((double) j->m0, (double) (h + 1)) : pow((double) j->m1, (double) (2 * (h - j->n_head_log2) + 1)))
+        : 1.0;
+    const uint16_t * mp = NULL;
+    if (a->mask.data) {
+        const al_tensor * m = &a->mask;
+        mp = (const uint16_t *) ((const char *) m->data + iq1 * m->nb[1] + (iq2 % m->ne[2]) * m->nb[2] + (iq3 % m->ne[3]) * m->nb[3]);
+    }
+    const int64_t ik3 = iq3 / j->rk3, ik2 = iq2 / j->rk2;
+    const int64_t iv3 = iq3 / j->rv3, iv2 = iq2 / j->rv2;
+    const float * pq = (const float *) ((const char *) a->q.data + iq1 * a->q.nb[1] + iq2 * a->q.nb[2] + iq3 * a->q.nb[3]);
+    for (int64_t d = 0; d < D; ++d) Q_q[d] = orc_f32_to_f16(pq[d]);
+    double M = -INFINITY;
+    for (int64_t ic = 0; ic < j->n_kv; ++ic) {
+        double mv = 0.0;
+        if (ic >= j->kv_len || (a->causal_pos0 >= 0 && ic > a->causal_pos0 + iq1)) mv = -INFINITY;
+        else if (mp) {
+            const double mval = (double) orc_f16_to_f32(mp[ic]);
+            mv = (mval == -INFINITY) ? -INFINITY : slope * mval;
+        }
+        if (mv == -INFINITY) { sc[ic] = -INFINITY; continue; }
+        const uint16_t * kd = (const uint16_t *) ((const char *) a->k.data + ic * a->k.nb[1] + ik2 * a->k.nb[2] + ik3 * a->k.nb[3]);
+        double s = 0.0;
+        for (int64_t d = 0; d < D; ++d) s += (double) orc_f16_to_f32(kd[d]) * (double) orc_f16_to_f32(Q_q[d]);
+        s *= (double) j->scale;
+        if (j->softcap != 0.0f) s = (double) j->softcap * tanh(s);
+        s += mv;
+        sc[ic] = s;
+        if (s > M) M = s;
+    }
+    double sink = -INFINITY;
+    if (a->sinks.data) {
+        sink = (double) ((const float *) a->sinks.data)[h];
+        if (sink > M) M = sink;
+    }
+    double S = 0.0;
+    for (int64_t d = 0; d < DV; ++d) acc[d] = 0.0;
+    for (int64_t ic = 0; ic < j->n_kv; ++ic) {
+        if (sc[ic] == -INFINITY) continue;
+        const double p = exp(sc[ic] - M);
+        const uint16_t * vd = (const uint16_t *) ((const char *) a->v.data + ic * a->v.nb[1] + iv2 * a->v.nb[2] + iv3 * a->v.nb[3]);
+        for (int64_t d = 0; d < DV; ++d) acc[d] += p * (double) orc_f16_to_f32(vd[d]);
+        S += p;
+    }
+    if (a->sinks.data) S += exp(sink - M);
+    float * out = (float *) ((char *) a->dst.data + (iq3 * T * Hq + iq2 + iq1 * Hq) * a->dst.nb[1]);
+    for (int64_t d = 0; d < DV; ++d) out[d] = (float) (acc[d] / S);   /* S == 0: NaN, as the reference */
+}
+
+typedef struct { const job_t * j; int ith; } worker_t;
+
+static void * worker(void * p) {
+    const worker_t * w = (const worker_t *) p;
+    const job_t * j = w->j;
+    const int64_t nr = j->T * j->Hq * j->B;
+    const int64_t dr = (nr + j->nth - 1) / j->nth;                        /* arm.cpp:2250-2257 */
+    const int64_t ir0 = dr * w->ith;
+    const int64_t ir1 = ir0 + dr < nr ? ir0 + dr : nr;
+    const int64_t DD = j->D > j->DV ? j->D : j->DV;
+    if (j->mode == 1) {
+        double * sc = (double *) malloc((size_t) j->n_kv * sizeof(double));
+        double * acc = (double *) malloc((size_t) DD * sizeof(double));
+        uint16_t * Q_q = (uint16_t *) malloc((size_t) DD * 2);
+        for (int64_t ir = ir0; ir < ir1; ++ir) row_o1(j, ir, sc, acc, Q_q);
+        free(sc); free(acc); free(Q_q);
+    } else {
+        float * VKQ32 = (float *) malloc((size_t) DD * 4);
+        uint16_t * VKQ16 = (uint16_t *) malloc((size_t) DD * 2);
+        uint16_t * Q_q = (uint16_t *) malloc((size_t) DD * 2);
+        for (int64_t ir = ir0; ir < ir1; ++ir) row_o2_o3(j, ir, VKQ32, VKQ16, Q_q);
+        free(VKQ32); free(VKQ16); free(Q_q);
+    }
+    return NULL;
+}
+
+static int run(const al_fattn_args * a, int n_threads, int mode) {
+    job_t j;
+    const int rc = prepare(&j, a, n_threads, mode);
+    if (rc != AL_OK) return rc;
+    pthread_t * th = (pthread_t *) malloc(sizeof(pthread_t) * (size_t) j.nth);
+    worker_t * ws = (worker_t *) malloc(sizeof(worker_t) * (size_t) j.nth);
+    for (int i = 0; i < j.nth; ++i) { ws[i].j = &j; ws[i].ith = i; }
+    for (int i = 1; i < j.nth; ++i) pthread_create(&th[i], NULL, worker, &ws[i]);
+    worker(&ws[0]);
+    for (int i = 1; i < j.nth; ++i) pthread_join(th[i], NULL);
+    free(th); free(ws);
+    return AL_OK;
+}
+
+int orc_fattn_o2(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 2); }
+int orc_fattn_o1(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 1); }
+int orc_fattn_o3(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 3); }
+
+/* set_rows f32 -> f16 (ops.cpp:135-181), single thread */
+int orc_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src, const al_tensor * idx) {
+    if (src->type != AL_TYPE_F32 || dst->type != AL_TYPE_F16) return AL_ERR_UNSUPPORTED;
+    if (idx->type != AL_TYPE_I64 && idx->type != AL_TYPE_I32) return AL_ERR_UNSUPPORTED;
+    const int64_t nc = src->ne[0], nr = src->ne[1];
+    if (dst->ne[0] != nc || dst->ne[2] != src->ne[2] || dst->ne[3] != src->ne[3]) return AL_ERR_INVALID;
+    if (src->ne[2] % idx->ne[1] != 0 || src->ne[3] % idx->ne[2] != 0) return AL_ERR_INVALID;
+    for (int64_t i03 = 0; i03 < src->ne[3]; ++i03)
+        for (int64_t i02 = 0; i02 < src->ne[2]; ++i02)
+            for (int64_t i = 0; i < nr; ++i) {
+                const int64_t i12 = i03 % idx->ne[2], i11 = i02 % idx->ne[1];
+                const char * ip = (const char *) idx->data + i * idx->nb[0] + i11 * idx->nb[1] + i12 * idx->nb[2];
+                const int64_t i1 = idx->type == AL_TYPE_I64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+                if (i1 < 0 || i1 >= dst->ne[1]) return AL_ERR_INVALID;
+                const float * s = (const float *) ((const char *) src->data + i * src->nb[1] + i02 * src->nb[2] + i03 * src->nb[3]);
+                uint16_t * d = (uint16_t *) ((char *) dst->data + i1 * dst->nb[1] + i02 * dst->nb[2] + i03 * dst->nb[3]);
+                for (int64_t c = 0; c < nc; ++c) d[c] = orc_f32_to_f16(s[c]);
+            }
+    return AL_OK;
+}

@@ -1,0 +1,53 @@
+/*
+ * fattn_oracle.h - CPU oracle for the flash-attention path (TEST
+ * INFRASTRUCTURE ONLY).
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this library, and only as the checker or the CPU baseline. The
+ * product path (arclight_amd, libarclight_fattn.so) never calls it.
+ *
+ * Three restatements of ArcLight's nnml_compute_forward_flash_attn_ext_f16
+ * (nnml/src/ops/arm/arm.cpp:2196-2433):
+ *   O2  orc_fattn_o2  line-for-line control flow of the reference (row split
+ *                     over threads, online softmax with the s > M branch,
+ *                     mask skip, sinks, ALiBi, softcap, permuted store) with
+ *                     Q rounded to f16 (common.cpp:19-24) and f32 accumulation
+ *                     of Q.K and V. THE PARITY ORACLE.
+ *   O1  orc_fattn_o1  fp64 brute force: two-pass softmax over visible cells.
+ *   O3  orc_fattn_o3  ARM-faithful diagnostic: f16 FMA dot lanes
+ *                     (arm.cpp:89-124, 358-376) and an f16 V accumulator
+ *                     (arm.cpp:1503-1551, 1655-1755). Not a parity target.
+ * All three take the product's al_fattn_args with HOST pointers, including
+ * the kv_len / causal_pos0 masking rules documented in arclight_fattn.h.
+ */
+#ifndef ARCLIGHT_FATTN_ORACLE_H
+#define ARCLIGHT_FATTN_ORACLE_H
+
+#include <stdint.h>
+#include "../include/arclight_fattn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* IEEE binary16 conversions, round-to-nearest-even
+ * (restating nnml/include/ops.h:276-323). */
+uint16_t orc_f32_to_f16(float f);
+float    orc_f16_to_f32(uint16_t h);
+void     orc_f32_to_f16_n(const float * x, uint16_t * y, int64_t n);
+void     orc_f16_to_f32_n(const uint16_t * x, float * y, int64_t n);
+
+/* Attention oracles; return 0 or a negative al status. n_threads >= 1. */
+int orc_fattn_o2(const al_fattn_args * a, int n_threads);
+int orc_fattn_o1(const al_fattn_args * a, int n_threads);
+int orc_fattn_o3(const al_fattn_args * a, int n_threads);
+
+/* set_rows f32 -> f16 (nnml/src/ops/ops.cpp:135-181). */
+int orc_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
+                         const al_tensor * idx);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,165 @@
+"""Python binding of the CPU oracle (TEST INFRASTRUCTURE ONLY).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, as the checker or as the timed CPU baseline. The product package
+(arclight_amd) never imports it.
+
+Arrays use the physical layouts documented in arclight_amd.abi:
+q (B, T, Hq, D) f32; k, v (B, n_kv, Hkv, D) f16; mask (m3, m2, rows, n_kv)
+f16; sinks (Hq,) f32; the result is (B, T, Hq, D) f32.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from arclight_amd import abi
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_build", "liborc_fattn.so")
+
+_lib = None
+
+
+def build():
+    """Compiles the oracle library with its Makefile."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.orc_f32_to_f16.restype = ctypes.c_uint16
+        L.orc_f32_to_f16.argtypes = [ctypes.c_float]
+        L.orc_f16_to_f32.restype = ctypes.c_float
+        L.orc_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.orc_f32_to_f16_n.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_f16_to_f32_n.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        for name in ("orc_fattn_o1", "orc_fattn_o2", "orc_fattn_o3"):
+            f = getattr(L, name)
+            f.restype = ctypes.c_int
+            f.argtypes = [ctypes.POINTER(abi.AlFattnArgs), ctypes.c_int]
+        L.orc_set_rows_f32_f16.restype = ctypes.c_int
+        L.orc_set_rows_f32_f16.argtypes = [ctypes.POINTER(abi.AlTensor)] * 3
+        _lib = L
+    return _lib
+
+
+def f32_to_f16_bits(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_n(x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def f16_bits_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    y = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32_n(h.ctypes.data, y.ctypes.data, h.size)
+    return y
+
+
+def _bits(a):
+    if a.dtype == np.float16:
+        return a.view(np.uint16)
+    if a.dtype != np.uint16:
+        raise TypeError("f16 operand must be float16 or uint16 bits")
+    return a
+
+
+def default_threads():
+    n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def build_args(q, k, v, mask=None, sinks=None, dst=None, *, scale, max_bias=0.0,
+               logit_softcap=0.0, kv_len=0, causal_pos0=-1, prec=abi.AL_PREC_F32):
+    """al_fattn_args over host numpy arrays (kept alive by the caller)."""
+    a = abi.AlFattnArgs()
+    a.q = abi.tensor_desc(q.ctypes.data, abi.AL_TYPE_F32, q.shape, q.strides, abi.Q_AXES)
+    a.k = abi.tensor_desc(k.ctypes.data, abi.AL_TYPE_F16, k.shape, k.strides, abi.KV_AXES)
+    a.v = abi.tensor_desc(v.ctypes.data, abi.AL_TYPE_F16, v.shape, v.strides, abi.KV_AXES)
+    a.mask = (abi.tensor_desc(mask.ctypes.data, abi.AL_TYPE_F16, mask.shape, mask.strides, abi.MASK_AXES)
+              if mask is not None else abi.empty_tensor())
+    a.sinks = (abi.make_tensor(sinks.ctypes.data, abi.AL_TYPE_F32, [sinks.shape[0]])
+               if sinks is not None else abi.empty_tensor())
+    a.dst = abi.tensor_desc(dst.ctypes.data, abi.AL_TYPE_F32, dst.shape, dst.strides, abi.DST_AXES)
+    a.scale = scale
+    a.max_bias = max_bias
+    a.logit_softcap = logit_softcap
+    a.prec = prec
+    a.kv_len = kv_len
+    a.causal_pos0 = causal_pos0
+    return a
+
+
+def attention(q, k, v, mask=None, sinks=None, *, scale, max_bias=0.0, logit_softcap=0.0,
+              kv_len=0, causal_pos0=-1, mode="o2", threads=None, prec=abi.AL_PREC_F32):
+    """Runs oracle O1 / O2 / O3 and returns dst as (B, T, Hq, D) f32."""
+    assert q.dtype == np.float32 and q.ndim == 4
+    k = _bits(k)
+    v = _bits(v)
+    if mask is not None:
+        mask = _bits(mask)
+    if sinks is not None:
+        sinks = np.ascontiguousarray(sinks, dtype=np.float32)
+    B, T, Hq, _ = q.shape
+    D = v.shape[3]
+    dst = np.full((B, T, Hq, D), np.nan, dtype=np.float32)
+    a = build_args(q, k, v, mask, sinks, dst, scale=scale, max_bias=max_bias,
+                   logit_softcap=logit_softcap, kv_len=kv_len, causal_pos0=causal_pos0, prec=prec)
+    fn = {"o1": lib().orc_fattn_o1, "o2": lib().orc_fattn_o2, "o3": lib().orc_fattn_o3}[mode]
+    rc = fn(ctypes.byref(a), threads or default_threads())
+    if rc != 0:
+        raise ValueError(f"oracle {mode} rejected the operands: {abi.STATUS_NAMES.get(rc, rc)}")
+    return dst
+
+
+def set_rows(cache, rows, idx):
+    """Oracle of the KV write: cache (n_rows_dst, nc) f16 bits, rows (n, nc)
+    f32, idx (n,) int64/int32. Returns a new cache array."""
+    out = np.array(_bits(cache), copy=True)
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    idx = np.ascontiguousarray(idx)
+    it = abi.AL_TYPE_I64 if idx.dtype == np.int64 else abi.AL_TYPE_I32
+    dst = abi.make_tensor(out.ctypes.data, abi.AL_TYPE_F16, [out.shape[1], out.shape[0]])
+    src = abi.make_tensor(rows.ctypes.data, abi.AL_TYPE_F32, [rows.shape[1], rows.shape[0]])
+    ix = abi.make_tensor(idx.ctypes.data, it, [idx.shape[0]])
+    rc = lib().orc_set_rows_f32_f16(ctypes.byref(dst), ctypes.byref(src), ctypes.byref(ix))
+    if rc != 0:
+        raise ValueError(f"oracle set_rows rejected the operands: {abi.STATUS_NAMES.get(rc, rc)}")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# Seeded synthetic inputs and masks (host side).
+# ---------------------------------------------------------------------------
+
+def make_inputs(seed, *, B=1, T=1, Hq=32, Hkv=8, D=128, n_kv=512, kv_size=None):
+    """q ~ N(0,1) f32 (B, T, Hq, D); k, v ~ N(0,1) rounded to f16 (RNE) in a
+    cell-major cache of kv_size cells, returned as views of the first n_kv."""
+    kv_size = kv_size or n_kv
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((B, T, Hq, D), dtype=np.float32)
+    kc = rng.standard_normal((B, kv_size, Hkv, D), dtype=np.float32).astype(np.float16)
+    vc = rng.standard_normal((B, kv_size, Hkv, D), dtype=np.float32).astype(np.float16)
+    return q, kc[:, :n_kv], vc[:, :n_kv]
+
+
+def causal_mask(T, n_kv, pos0, kv_len=None, n_stream=1):
+    """f16 mask (n_stream, 1, PAD(T, 64), n_kv) of 0 / -inf, filled as
+    set_inputs_attn_mask (nnml/src/cgraph.cpp:1224-1261) does for one
+    contiguous sequence whose token t sits at position pos0 + t and whose
+    cells hold positions 0..kv_len-1."""
+    kv_len = n_kv if kv_len is None else kv_len
+    rows = (T + 63) // 64 * 64
+    m = np.full((n_stream, 1, rows, n_kv), -np.inf, dtype=np.float16)
+    c = np.arange(n_kv)
+    for t in range(T):
+        vis = (c < kv_len) & (c <= pos0 + t)
+        m[:, 0, t, vis] = 0.0
+    return m

@@ -1,0 +1,183 @@
+"""GPU parity of al_fattn_f16 against oracle O2 (the f32-accumulating
+restatement of nnml_compute_forward_flash_attn_ext_f16, arm.cpp:2196-2433).
+
+Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the fp32 output, identical NaN
+pattern. Every case prints its name before touching the GPU.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from arclight_amd import abi
+from oracle import oracle as O
+from tests.fattn_cases import assert_parity, run_gpu
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / math.sqrt(128)
+
+
+def _case(name):
+    print(f"\n[case] {name}", flush=True)
+
+
+def _check(name, q, k, v, mask=None, sinks=None, **kw):
+    _case(name)
+    ref = O.attention(q, k, v, mask, sinks, **kw)
+    got = run_gpu(q, k, v, mask, sinks, **kw)
+    assert_parity(got, ref, what=name)
+    return got, ref
+
+
+@pytest.mark.parametrize("explicit", [True, False])
+def test_decode_qwen3_4b_c512(gpu, explicit):
+    # 1 layer, q_len 1, Hq 32, Hkv 8, D 128, context 512 (+ the new token), n_kv padded to 768
+    q, k, v = O.make_inputs(1234, T=1, Hq=32, Hkv=8, n_kv=768)
+    if explicit:
+        _check("decode c512 explicit mask", q, k, v, O.causal_mask(1, 768, 512), scale=SCALE)
+    else:
+        _check("decode c512 implicit", q, k, v, scale=SCALE, kv_len=513)
+
+
+@pytest.mark.parametrize("ctx", [4096, 32768])
+def test_decode_qwen3_4b_long(gpu, ctx):
+    q, k, v = O.make_inputs(ctx, T=1, Hq=32, Hkv=8, n_kv=ctx)
+    _check(f"decode ctx {ctx}", q, k, v, scale=SCALE, kv_len=ctx)
+
+
+def test_decode_gqa8_qwen3_32b(gpu):
+    q, k, v = O.make_inputs(7, T=1, Hq=64, Hkv=8, n_kv=4096)
+    _check("decode gqa 8:1 ctx 4096", q, k, v, scale=SCALE)
+
+
+@pytest.mark.parametrize("T", [2, 4, 8])
+def test_verify_qwen3_8b(gpu, T):
+    # speculative verify: drafts at positions C..C+T-1, causal among drafts
+    C = 2048
+    n_kv = 2304
+    q, k, v = O.make_inputs(100 + T, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    _check(f"verify T={T} explicit", q, k, v, O.causal_mask(T, n_kv, C), scale=SCALE)
+    _check(f"verify T={T} implicit", q, k, v, scale=SCALE, kv_len=C + T, causal_pos0=C)
+
+
+def test_verify_gqa8_t8(gpu):
+    q, k, v = O.make_inputs(55, T=8, Hq=64, Hkv=8, n_kv=1024)
+    _check("verify gqa8 T=8", q, k, v, scale=SCALE, kv_len=1000, causal_pos0=992)
+
+
+@pytest.mark.parametrize("T,pos0", [(64, 0), (96, 160)])
+def test_prefill_chunk_causal(gpu, T, pos0):
+    n_kv = pos0 + T
+    q, k, v = O.make_inputs(T + pos0, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    _check(f"prefill T={T} pos0={pos0} explicit", q, k, v, O.causal_mask(T, n_kv, pos0), scale=SCALE)
+    _check(f"prefill T={T} pos0={pos0} implicit", q, k, v, scale=SCALE, causal_pos0=pos0)
+
+
+def test_streams_and_mask_broadcast(gpu):
+    # two streams (nnml dim 3) with their own mask planes
+    rng = np.random.default_rng(3)
+    q, k, v = O.make_inputs(3, B=2, T=2, Hq=8, Hkv=2, n_kv=256)
+    m = np.full((2, 1, 64, 256), -np.inf, dtype=np.float16)
+    m[0, 0, :2, :100] = 0
+    m[1, 0, :2, 50:230] = 0
+    m[1, 0, 1, 229] = -np.inf
+    _check("streams B=2", q, k, v, m, scale=SCALE)
+    # per-head mask planes with finite values
+    mh = rng.uniform(-3, 0, size=(1, 8, 64, 256)).astype(np.float16)
+    mh[..., 200:] = -np.inf
+    _check("mask per head", q, k, v, mh, scale=SCALE)
+
+
+def test_sinks_softcap_alibi(gpu):
+    rng = np.random.default_rng(11)
+    q, k, v = O.make_inputs(11, T=3, Hq=12, Hkv=4, n_kv=320)
+    sinks = rng.standard_normal(12).astype(np.float32) * 3
+    m = O.causal_mask(3, 320, 300)
+    _check("sinks", q, k, v, m, sinks, scale=SCALE)
+    _check("softcap", q, k, v, m, scale=SCALE * 4, logit_softcap=5.0)
+    alibi = m.astype(np.float32)
+    alibi[0, 0, :3, :301] = -np.arange(301, dtype=np.float32)[::-1] / 64.0
+    _check("alibi", q, k, v, alibi.astype(np.float16), scale=SCALE, max_bias=8.0)
+
+
+def test_ragged_sizes(gpu):
+    # n_kv not a multiple of 32, kv_len not a multiple of the tile, T*G = 12 rows
+    q, k, v = O.make_inputs(5, T=3, Hq=8, Hkv=2, n_kv=40)
+    _check("n_kv 40 kv_len 37", q, k, v, scale=SCALE, kv_len=37)
+    q, k, v = O.make_inputs(6, T=5, Hq=6, Hkv=3, n_kv=33)
+    _check("n_kv 33 T 5 G 2", q, k, v, O.causal_mask(5, 33, 27), scale=SCALE)
+
+
+def test_all_masked_rows_are_nan_and_single_cell(gpu):
+    q, k, v = O.make_inputs(9, T=2, Hq=4, Hkv=1, n_kv=64)
+    m = np.full((1, 1, 64, 64), -np.inf, dtype=np.float16)
+    m[0, 0, 1, 17] = 0                      # token 1 sees exactly cell 17, token 0 sees nothing
+    got, ref = _check("all-masked + single cell", q, k, v, m, scale=SCALE)
+    assert np.isnan(got[0, 0]).all()
+    vf = v.astype(np.float32)
+    np.testing.assert_allclose(got[0, 1], np.broadcast_to(vf[0, 17, 0], (4, 128)), rtol=0, atol=1e-6)
+
+
+def test_garbage_in_masked_cells(gpu):
+    # unwritten cache cells may hold NaN/Inf: masked cells must not leak
+    q, k, v = O.make_inputs(21, T=1, Hq=32, Hkv=8, n_kv=512)
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=300)
+    kg, vg = k.copy(), v.copy()
+    kg[:, 300:] = np.float16(np.nan)
+    vg[:, 300:] = np.float16(np.inf)
+    _case("garbage beyond kv_len")
+    got = run_gpu(q, kg, vg, scale=SCALE, kv_len=300)
+    assert_parity(got, ref, what="garbage")
+    m = O.causal_mask(1, 512, 299)
+    _case("garbage beyond mask")
+    got = run_gpu(q, kg, vg, m, scale=SCALE)
+    assert_parity(got, ref, what="garbage mask")
+
+
+def test_prec_default_and_determinism(gpu):
+    q, k, v = O.make_inputs(31, T=1, Hq=32, Hkv=8, n_kv=2048)
+    _case("determinism")
+    a = run_gpu(q, k, v, scale=SCALE, prec=abi.AL_PREC_DEFAULT)
+    b = run_gpu(q, k, v, scale=SCALE, prec=abi.AL_PREC_F32)
+    assert np.array_equal(a, b)
+
+
+def test_caller_workspace(gpu):
+    from arclight_amd import device, fattn
+    from arclight_amd._lib import ArclightError
+    q, k, v = O.make_inputs(41, T=1, Hq=32, Hkv=8, n_kv=8192)
+    ref = O.attention(q, k, v, scale=SCALE)
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    dst = device.DeviceTensor.empty(q.shape, np.float32, axes=abi.DST_AXES)
+    need = fattn.workspace_bytes(dq, dk, dv, None, None, dst, scale=SCALE)
+    assert need > 0
+    _case("caller workspace")
+    ws = device.DeviceBuffer(need)
+    ws.zero()
+    for _ in range(2):
+        fattn.flash_attn_ext(dq, dk, dv, scale=SCALE, dst=dst, workspace=ws)
+        device.synchronize()
+        assert_parity(dst.numpy(np.float32), ref, what="caller workspace")
+    small = device.DeviceBuffer(need - 4)
+    with pytest.raises(ArclightError) as ei:
+        fattn.flash_attn_ext(dq, dk, dv, scale=SCALE, dst=dst, workspace=small)
+    assert ei.value.status == abi.AL_ERR_WORKSPACE
+
+
+def test_rejects_what_the_reference_asserts(gpu):
+    from arclight_amd._lib import ArclightError
+    q, k, v = O.make_inputs(1, T=2, Hq=8, Hkv=3 if False else 2, n_kv=64)
+    short_mask = np.zeros((1, 1, 32, 64), dtype=np.float16)     # rows < PAD(T, 64)
+    with pytest.raises(ArclightError) as ei:
+        run_gpu(q, k, v, short_mask, scale=SCALE)
+    assert ei.value.status == abi.AL_ERR_INVALID
+    with pytest.raises(ArclightError) as ei:
+        run_gpu(q, k, v, scale=SCALE, max_bias=1.0)              # ALiBi without mask
+    assert ei.value.status == abi.AL_ERR_INVALID
+    with pytest.raises(ArclightError) as ei:
+        run_gpu(q, k, v, scale=SCALE, prec=3)
+    assert ei.value.status == abi.AL_ERR_INVALID
+    q64, k64, v64 = O.make_inputs(1, T=1, Hq=8, Hkv=2, D=64, n_kv=64)
+    with pytest.raises(ArclightError) as ei:
+        run_gpu(q64, k64, v64, scale=SCALE)
+    assert ei.value.status == abi.AL_ERR_UNSUPPORTED
