@@ -119,6 +119,8 @@ static int library_workspace(size_t bytes, void ** ptr) {
         if (e != hipSuccess) return al_fail(AL_ERR_HIP, "hipMalloc(workspace %zu bytes): %s", sz, hipGetErrorString(e));
         e = hipMemset(st->ws, 0, sz);
         if (e != hipSuccess) return al_hip_fail(e, "hipMemset(workspace)");
+        e = hipDeviceSynchronize();               // zeroed before any stream's kernel uses it
+        if (e != hipSuccess) return al_hip_fail(e, "hipDeviceSynchronize");
         st->ws_bytes = sz;
     }
     *ptr = st->ws;
@@ -203,6 +205,9 @@ int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
         return al_fail(AL_ERR_UNSUPPORTED, "fattn: operands must be 16-byte aligned with 16-byte multiple strides");
     if (n_kv <= 0 || n_kv > INT32_MAX / 2 || T <= 0 || T > (1 << 24) || B > 65535 || Hq * T > INT32_MAX / 2)
         return al_fail(AL_ERR_UNSUPPORTED, "fattn: sizes out of range");
+    // K/V of one (stream, head) are addressed with 32-bit buffer offsets
+    if ((uint64_t) (n_kv - 1) * k.nb[1] + 256 > (uint64_t) INT32_MAX || (uint64_t) (n_kv - 1) * v.nb[1] + 256 > (uint64_t) INT32_MAX)
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn: one head's K/V view spans more than 2 GiB");
 
     Plan pl;
     FattnParams & p = pl.p;
@@ -238,16 +243,19 @@ int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
     extent = std::max<int64_t>(extent, 0);
     const int64_t tiles = (extent + 31) / 32;
     const int64_t units = (int64_t) Hkv * p.n_row_tiles * B;
+    const int64_t waves = fattn_splitkv_waves(pl.rows_per_tile);
     const int64_t target = (int64_t) n_cu * wgs_per_cu();
     int64_t n_split = (target + units - 1) / units;
-    n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, (tiles + 3) / 4));
-    int64_t cps_tiles = (tiles + n_split - 1) / n_split;
-    cps_tiles = std::max<int64_t>(cps_tiles, 1);
+    // every wave of a split gets at least one 32-cell tile
+    n_split = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(n_split, (tiles + waves - 1) / waves), kFattnMaxSplit));
+    int64_t cps_tiles = std::max<int64_t>(1, (tiles + n_split - 1) / n_split);
     p.cells_per_split = (int32_t) (cps_tiles * 32);
     n_split = std::max<int64_t>(1, (extent + p.cells_per_split - 1) / p.cells_per_split);
+    if ((size_t) units * sizeof(unsigned) > kFattnCounterBytes) n_split = 1;
+    if (n_split == 1) p.cells_per_split = (int32_t) std::max<int64_t>(32, (extent + 31) / 32 * 32);
     p.n_split = (int32_t) n_split;
     if (p.n_split > 1) {
-        pl.counters_bytes = ((size_t) units * sizeof(unsigned) + 255) & ~(size_t) 255;
+        pl.counters_bytes = kFattnCounterBytes;
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
     }
     *out = pl;

@@ -48,3 +48,33 @@ __device__ __forceinline__ float colsum4(float x) {
     x += __shfl_xor(x, 32);
     return x;
 }
+
+// Hand-off of merge records between workgroups of one launch. Records are
+// written and read with agent-scope (device-coherent) relaxed atomic stores
+// and loads, which gfx950 performs at the device coherence point (stores
+// write through the writer's L2, loads do not return stale lines of the
+// reader's L2), so no L2-wide writeback or invalidate is needed. A writer
+// waits for its stores to complete (s_waitcnt) before a barrier and the
+// relaxed arrival-counter update; the workgroup that sees the final count
+// reads the records only after that update returned. This is the ordering
+// the compiler itself relies on for agent-scope atomics (a completed
+// agent-scope store is visible to agent-scope loads of every CU).
+__device__ __forceinline__ void st_agent(float * p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float * p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned add_agent(unsigned * p, unsigned v) {
+    return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent_u32(unsigned * p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Keeps the compiler from moving this wave's memory accesses across it and
+// waits until all of them have completed (s_waitcnt 0).
+__device__ __forceinline__ void complete_wave_memops() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+}
+__device__ __forceinline__ void order_after_counter() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup"); }

@@ -28,13 +28,21 @@ struct FattnParams {
     int32_t n_row_tiles;
     int32_t n_split;
     int32_t cells_per_split;        // multiple of 32
-    float *    part;                // split-KV merge records
-    unsigned * counters;            // one per (stream, kv head, row tile), zero between calls
+    float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
+    unsigned * counters;            // [units] in the fixed counter region, zero between calls
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).
 int fattn_splitkv_rows_per_tile(int R);
+// Wavefronts per workgroup of the split-KV kernel for a rows-per-tile value.
+int fattn_splitkv_waves(int rows_per_tile);
 hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
 
 // Floats of one split-KV merge record row (O[128], m, l, pad).
 constexpr int kFattnRecordStride = 132;
+// At most kFattnMaxSplit splits per row tile; one merge level.
+constexpr int kFattnMaxSplit = 32;
+// Every workspace starts with a fixed arrival-counter region, so that no
+// call's merge records ever overlap another call's counters; kernels leave
+// it zeroed. Records follow it.
+constexpr size_t kFattnCounterBytes = 256u << 10;

@@ -1,0 +1,302 @@
+#!/usr/bin/env python3
+"""Benchmark of the flash-attention op on one MI355X.
+
+Step = the decode attention of one token through all 36 layers of a
+Qwen3-4B-shaped model (32 query heads, 8 KV heads, head_dim 128) at 32K
+context: 36 al_fattn_f16 calls back to back on one stream, each layer with
+its own f16 cache slice (128 MiB per layer, 4.5 GiB in all, so every layer
+is read cold from HBM), replayed as one captured HIP graph.
+
+    python bench.py [--steps K] [--warmup W] [--ctx 32768]
+
+Prints one JSON line. `value` is the KV read bandwidth of the whole step:
+algorithmic bytes (K+V of the visible cells, + Q + O) / step time. Extra
+fields report 2048-token chunked causal prefill TFLOP/s (4 chunks of 512 over
+36 layers), the roofline of the decode kernel from per-launch HIP events, and
+the CPU baseline (the f32 restatement of the reference kernel on host cores).
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+F16_PEAK_TFLOPS = 2500.0       # MI355X dense f16 MFMA, TFLOP/s
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--ctx", type=int, default=32768)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
+    ap.add_argument("--only", choices=["decode", "prefill", "copy"], default=None,
+                    help="run one workload only (for profiling); prints its own JSON line")
+    return ap.parse_args()
+
+
+class Layers:
+    """Per-layer device operands of one attention call shape."""
+
+    def __init__(self, L, T, Hq, Hkv, D, n_kv, seed):
+        from arclight_amd import abi, device
+        self.L, self.T, self.Hq, self.Hkv, self.D, self.n_kv = L, T, Hq, Hkv, D, n_kv
+        from arclight_amd._lib import call
+        self.q, self.k, self.v, self.dst = [], [], [], []
+        for l in range(L):
+            q = device.DeviceTensor.empty((1, T, Hq, D), np.float32, axes=abi.Q_AXES)
+            k = device.DeviceTensor.empty((1, n_kv, Hkv, D), np.uint16, axes=abi.KV_AXES)
+            v = device.DeviceTensor.empty((1, n_kv, Hkv, D), np.uint16, axes=abi.KV_AXES)
+            d = device.DeviceTensor.empty((1, T, Hq, D), np.float32, axes=abi.DST_AXES)
+            call("al_util_fill_randn_f32", q.ptr, T * Hq * D, seed, 3 * l, None)
+            call("al_util_fill_randn_f16", k.ptr, n_kv * Hkv * D, seed, (3 * l + 1) << 40, None)
+            call("al_util_fill_randn_f16", v.ptr, n_kv * Hkv * D, seed, (3 * l + 2) << 40, None)
+            self.q.append(q); self.k.append(k); self.v.append(v); self.dst.append(d)
+        device.synchronize()
+
+    def args(self, l, stream, scale, kv_len, causal_pos0=-1, q=None, dst=None):
+        from arclight_amd import fattn
+        return fattn.fattn_args(q or self.q[l], self.k[l], self.v[l], None, None, dst or self.dst[l],
+                                scale=scale, kv_len=kv_len, causal_pos0=causal_pos0, stream=stream)
+
+
+def run_calls(lib, arg_list):
+    f = lib.al_fattn_f16
+    for a in arg_list:
+        rc = f(ctypes.byref(a))
+        if rc != 0:
+            raise RuntimeError(lib.al_last_error().decode())
+
+
+def time_graph(lib, stream, arg_list, steps, warmup):
+    """Captures one step into a HIP graph; returns (ms_per_step, graph_exec)."""
+    from arclight_amd import device
+    from arclight_amd._lib import call
+    run_calls(lib, arg_list)                      # allocates the workspace outside the capture
+    stream.synchronize()
+    call("al_util_graph_begin", stream.handle)
+    run_calls(lib, arg_list)
+    ge = ctypes.c_void_p()
+    call("al_util_graph_end", stream.handle, ctypes.byref(ge))
+    for _ in range(warmup):
+        call("al_util_graph_launch", ge.value, stream.handle)
+    stream.synchronize()
+    e0, e1 = device.Event(), device.Event()
+    device.synchronize()
+    e0.record(stream)
+    for _ in range(steps):
+        call("al_util_graph_launch", ge.value, stream.handle)
+    e1.record(stream)
+    e1.synchronize()
+    device.synchronize()
+    ms = e0.elapsed_ms(e1) / steps
+    call("al_util_graph_destroy", ge.value)
+    return ms
+
+
+def time_per_launch(lib, stream, arg_list, reps):
+    """Average kernel duration from an event pair around every launch."""
+    from arclight_amd import device
+    n = len(arg_list) * reps
+    ev = [(device.Event(), device.Event()) for _ in range(n)]
+    f = lib.al_fattn_f16
+    i = 0
+    device.synchronize()
+    for _ in range(reps):
+        for a in arg_list:
+            ev[i][0].record(stream)
+            f(ctypes.byref(a))
+            ev[i][1].record(stream)
+            i += 1
+    stream.synchronize()
+    d = [s.elapsed_ms(e) for s, e in ev]
+    for s, e in ev:
+        s.destroy(); e.destroy()
+    return float(np.mean(d)), float(np.median(d))
+
+
+def decode_bytes(ctx, Hq, Hkv, D, T=1):
+    return 2 * ctx * Hkv * D * 2 + 2 * T * Hq * D * 4
+
+
+def prefill_flops(T_total, chunk, Hq, D):
+    pairs = 0
+    for c in range(T_total // chunk):
+        pairs += chunk * chunk * c + chunk * (chunk + 1) // 2
+    return 4 * D * Hq * pairs
+
+
+def bench_decode(lib, stream, a):
+    Hq, Hkv, D, L, ctx = 32, 8, 128, a.layers, a.ctx
+    scale = 1.0 / math.sqrt(D)
+    lay = Layers(L, 1, Hq, Hkv, D, ctx, a.seed)
+    args = [lay.args(l, stream, scale, kv_len=ctx) for l in range(L)]
+    ms = time_graph(lib, stream, args, a.steps, a.warmup)
+    k_mean, k_med = time_per_launch(lib, stream, args, max(2, a.steps // 4))
+    byts = decode_bytes(ctx, Hq, Hkv, D)
+    return {
+        "ms_per_step": ms,
+        "bytes_per_layer": byts,
+        "gbs": byts * L / (ms * 1e-3) / 1e9,
+        "kernel_ms_mean": k_mean,
+        "kernel_ms_median": k_med,
+        "kernel_gbs": byts / (k_mean * 1e-3) / 1e9,
+    }
+
+
+def bench_prefill(lib, stream, a):
+    Hq, Hkv, D, L = 32, 8, 128, a.layers
+    T_total, chunk = 2048, 512
+    scale = 1.0 / math.sqrt(D)
+    lay = Layers(L, T_total, Hq, Hkv, D, T_total, a.seed + 1)
+    from arclight_amd import abi, device
+    args = []
+    for c in range(T_total // chunk):
+        for l in range(L):
+            # chunk c: tokens 512c..512c+511 against cells [0, 512(c+1)), causal within the chunk
+            q = lay.q[l]
+            qv = device.DeviceTensor(q.buf, abi.AL_TYPE_F32, (1, chunk, Hq, D), None,
+                                     c * chunk * Hq * D * 4, abi.Q_AXES)
+            dv = device.DeviceTensor(lay.dst[l].buf, abi.AL_TYPE_F32, (1, chunk, Hq, D), None,
+                                     c * chunk * Hq * D * 4, abi.DST_AXES)
+            args.append(lay.args(l, stream, scale, kv_len=chunk * (c + 1), causal_pos0=chunk * c, q=qv, dst=dv))
+    ms = time_graph(lib, stream, args, max(1, a.steps // 2), max(1, a.warmup))
+    k_mean, _ = time_per_launch(lib, stream, args, 1)
+    fl = prefill_flops(T_total, chunk, Hq, D)
+    return {"ms_per_step": ms, "flops_per_layer": fl, "tflops": fl * L / (ms * 1e-3) / 1e12,
+            "kernel_ms_mean": k_mean}
+
+
+def bench_copy(stream, nbytes=1 << 30):
+    """Plain device copy of known size (calibrates rocprof byte counters)."""
+    from arclight_amd import device
+    from arclight_amd._lib import call
+    a_, b_ = device.DeviceBuffer(nbytes), device.DeviceBuffer(nbytes)
+    call("al_util_memset", a_.ptr, 1, nbytes)
+    e0, e1 = device.Event(), device.Event()
+    for _ in range(2):
+        call("al_util_memcpy_d2d", b_.ptr, a_.ptr, nbytes, stream.handle)
+    e0.record(stream)
+    reps = 10
+    for _ in range(reps):
+        call("al_util_memcpy_d2d", b_.ptr, a_.ptr, nbytes, stream.handle)
+    e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / reps
+    return {"bytes": nbytes, "ms": ms, "gbs": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+def cpu_baseline(a):
+    """Oracle O2 (f32 restatement of arm.cpp:2196-2433) on host cores,
+    decode at the same shape on a bounded sample of layers."""
+    from oracle import oracle as O
+    threads = min(16, os.cpu_count() or 1)
+    Hq, Hkv, D, ctx = 32, 8, 128, a.ctx
+    n_layers = 2
+    data = [O.make_inputs(a.seed + l, T=1, Hq=Hq, Hkv=Hkv, D=D, n_kv=ctx) for l in range(n_layers)]
+    scale = 1.0 / math.sqrt(D)
+    O.attention(*data[0], scale=scale, kv_len=ctx, threads=threads)     # warm
+    t0 = time.perf_counter()
+    calls = 0
+    while True:
+        for q, k, v in data:
+            O.attention(q, k, v, scale=scale, kv_len=ctx, threads=threads)
+            calls += 1
+        el = time.perf_counter() - t0
+        if el >= a.cpu_seconds or calls >= 400:
+            break
+    per = el / calls
+    byts = decode_bytes(ctx, Hq, Hkv, D)
+    return {"value": byts / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"decode ctx {ctx}, {calls} single-layer calls over {n_layers} distinct layers, "
+                      f"{el:.1f} s, {per * 1e3:.1f} ms/layer"}
+
+
+def load_traffic():
+    p = os.path.join(ROOT, "profiles", "decode_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f)
+    return None
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                          "(attention would shard by KV head across GPUs, see DESIGN.md)"}))
+        sys.exit(2)
+    from arclight_amd import _lib, device
+    lib = _lib.load()
+    info = device.device_info()
+    stream = device.Stream()
+    print(f"[bench] {info}", file=sys.stderr, flush=True)
+
+    if a.only == "copy":
+        print(json.dumps({"copy": bench_copy(stream)}))
+        return
+    if a.only == "prefill":
+        print(json.dumps({"prefill": bench_prefill(lib, stream, a)}))
+        return
+
+    dec = bench_decode(lib, stream, a)
+    print(f"[bench] decode {dec}", file=sys.stderr, flush=True)
+    if a.only == "decode":
+        print(json.dumps({"decode": dec}))
+        return
+    pre = None if a.no_prefill else bench_prefill(lib, stream, a)
+    if pre:
+        print(f"[bench] prefill {pre}", file=sys.stderr, flush=True)
+    cpu = None if a.no_cpu_baseline else cpu_baseline(a)
+    if cpu:
+        print(f"[bench] cpu {cpu}", file=sys.stderr, flush=True)
+
+    traffic = load_traffic()
+    out = {
+        "metric": "decode-attn KV GB/s (% HBM peak) + prefill-attn TFLOP/s, Qwen3-4B shape",
+        "value": round(dec["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 K/V, f32 Q/O, f32 accumulation",
+        "data": "synthetic, seeded N(0,1)",
+        "config": {"workload": f"decode attention, Qwen3-4B shape (Hq 32, Hkv 8, D 128), batch 1, q_len 1, "
+                               f"context {a.ctx}, {a.layers} layers back to back, one cache slice per layer",
+                   "parallelism": "single GPU"},
+        "hbm_peak_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
+        "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
+                     "kernel": "fattn_splitkv_kernel<1,true>",
+                     "kernel_us_mean": round(dec["kernel_ms_mean"] * 1e3, 2),
+                     "algorithmic_bytes_per_launch": dec["bytes_per_layer"]},
+        "prefill": None if not pre else {
+            "workload": "2048-token causal prefill in 4 chunks of 512, 36 layers, Qwen3-4B shape",
+            "tflops": round(pre["tflops"], 2),
+            "mfma_peak_frac": round(pre["tflops"] / F16_PEAK_TFLOPS, 4),
+            "ms_per_step": round(pre["ms_per_step"], 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

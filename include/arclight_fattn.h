@@ -92,7 +92,10 @@ typedef struct al_tensor {
  *
  * workspace: device scratch for split-KV partials. NULL lets the library use
  * its own per-device buffer (allocated on first use, grown when needed).
- * Calls that share one workspace must be ordered on one stream.
+ * A caller workspace must be zero-filled before its first use: its first
+ * 256 KiB hold arrival counters that every call leaves at zero again, the
+ * rest holds per-call merge records. Calls that share one workspace must be
+ * ordered on one stream.
  */
 typedef struct al_fattn_args {
     al_tensor q;

@@ -181,3 +181,60 @@ def test_rejects_what_the_reference_asserts(gpu):
     with pytest.raises(ArclightError) as ei:
         run_gpu(q64, k64, v64, scale=SCALE)
     assert ei.value.status == abi.AL_ERR_UNSUPPORTED
+
+
+def test_split_merge_repeatable_back_to_back(gpu):
+    # Multi-split calls (two merge levels) launched back to back on one stream
+    # without host synchronization: every result must equal the first bit for
+    # bit (the merge order is fixed) and match the oracle.
+    from arclight_amd import device, fattn
+    q, k, v = O.make_inputs(77, T=1, Hq=32, Hkv=8, n_kv=32768)
+    ref = O.attention(q, k, v, scale=SCALE)
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    n = 64
+    dsts = [device.DeviceTensor.empty(q.shape, np.float32, axes=abi.DST_AXES) for _ in range(n)]
+    _case("split merge x64 back to back")
+    for rep in range(3):
+        for d in dsts:
+            fattn.flash_attn_ext(dq, dk, dv, scale=SCALE, dst=d)
+        device.synchronize()
+        outs = [d.numpy(np.float32) for d in dsts]
+        if rep == 0:
+            first = outs[0]
+            assert_parity(first, ref, what="split merge")
+        for i, o in enumerate(outs):
+            assert np.array_equal(o, first), f"rep {rep} call {i} differs"
+
+
+def test_shapes_alternating_on_one_workspace(gpu):
+    # Calls of different shapes lay out their merge records differently; the
+    # arrival counters live in a fixed region no record overlaps, so
+    # alternating shapes on one workspace keeps every call correct.
+    from arclight_amd import device, fattn
+    cases = [dict(seed=90, B=1, T=1, Hq=32, Hkv=8, n_kv=32768),
+             dict(seed=91, B=2, T=2, Hq=8, Hkv=2, n_kv=2048),
+             dict(seed=92, B=1, T=8, Hq=32, Hkv=8, n_kv=8192),
+             dict(seed=93, B=1, T=96, Hq=32, Hkv=8, n_kv=256)]
+    prepared = []
+    need = 0
+    for c in cases:
+        seed = c.pop("seed")
+        q, k, v = O.make_inputs(seed, **c)
+        ref = O.attention(q, k, v, scale=SCALE)
+        dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+        dst = device.DeviceTensor.empty(q.shape, np.float32, axes=abi.DST_AXES)
+        need = max(need, fattn.workspace_bytes(dq, dk, dv, None, None, dst, scale=SCALE))
+        prepared.append((dq, dk, dv, dst, ref))
+    ws = device.DeviceBuffer(need)
+    ws.zero()
+    _case("alternating shapes, one workspace")
+    for rnd in range(3):
+        for order in (prepared, prepared[::-1]):
+            for dq, dk, dv, dst, ref in order:
+                fattn.flash_attn_ext(dq, dk, dv, scale=SCALE, dst=dst, workspace=ws)
+            device.synchronize()
+            for i, (dq, dk, dv, dst, ref) in enumerate(order):
+                assert_parity(dst.numpy(np.float32), ref, what=f"round {rnd} call {i}")
+    cnt = np.empty(65536, dtype=np.uint32)
+    ws.download(cnt)
+    assert not cnt.any(), "arrival counters not left at zero"
