@@ -48,6 +48,7 @@ namespace {
 struct DeviceState {
     bool       init = false;
     int        n_cu = 0;
+    int        lds_per_block = 0;
     void *     ws = nullptr;        // library-owned split-KV workspace
     size_t     ws_bytes = 0;
     int *      err = nullptr;       // kernel-recorded errors (set_rows)
@@ -67,6 +68,8 @@ static int device_state(int * dev_out, DeviceState ** st_out) {
     DeviceState & st = g_dev[dev];
     if (!st.init) {
         e = hipDeviceGetAttribute(&st.n_cu, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return al_hip_fail(e, "hipDeviceGetAttribute");
+        e = hipDeviceGetAttribute(&st.lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
         if (e != hipSuccess) return al_hip_fail(e, "hipDeviceGetAttribute");
         e = hipMalloc((void **) &st.err, 256);
         if (e != hipSuccess) return al_hip_fail(e, "hipMalloc(error flag)");
@@ -94,6 +97,15 @@ int al_device_cu_count(int * n_cu) {
     const int rc = device_state(&dev, &st);
     if (rc != AL_OK) return rc;
     *n_cu = st->n_cu;
+    return AL_OK;
+}
+
+int al_device_lds_per_block(int * bytes) {
+    int dev;
+    DeviceState * st;
+    const int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    *bytes = st->lds_per_block;
     return AL_OK;
 }
 
@@ -135,12 +147,22 @@ namespace {
 
 struct Plan {
     FattnParams p;
+    bool prefill = false;
     int rows_per_tile = 16;
     size_t counters_bytes = 0;
     size_t part_bytes = 0;
 };
 
 bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
+
+// AL_FATTN_PREFILL=0 keeps many-row calls on the split-KV kernel.
+bool prefer_prefill() {
+    static bool v = [] {
+        const char * s = getenv("AL_FATTN_PREFILL");
+        return !(s && s[0] == '0');
+    }();
+    return v;
+}
 
 int wgs_per_cu() {
     static int v = [] {
@@ -154,7 +176,7 @@ int wgs_per_cu() {
 // Mirrors the asserts of nnml_flash_attn_ext (nnml/src/tensor.cpp:1292-1320)
 // and nnml_compute_forward_flash_attn_ext_f16 (arm.cpp:2213-2245), then the
 // limits of this path.
-int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
+int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) {
     if (!a) return al_fail(AL_ERR_INVALID, "fattn: null arguments");
     const al_tensor &q = a->q, &k = a->k, &v = a->v, &m = a->mask, &s = a->sinks, &d = a->dst;
     if (!q.data || !k.data || !v.data || !d.data) return al_fail(AL_ERR_INVALID, "fattn: q, k, v and dst are required");
@@ -235,6 +257,20 @@ int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
     p.m0 = powf(2.0f, -(p.max_bias) / p.n_head_log2);
     p.m1 = powf(2.0f, -(p.max_bias / 2.0f) / p.n_head_log2);
 
+    // Many query rows with implicit masking: the prefill kernel, one
+    // workgroup per 64-row tile, when that alone fills the device.
+    const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
+    if (!m.data && p.R > 32 && prefill_tiles * Hkv * B >= n_cu && lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
+        prefer_prefill()) {
+        pl.prefill = true;
+        pl.rows_per_tile = kFattnPrefillRows;
+        p.n_row_tiles = (int32_t) prefill_tiles;
+        p.n_split = 1;
+        p.cells_per_split = 0;
+        *out = pl;
+        return AL_OK;
+    }
+
     // split-KV sizing
     pl.rows_per_tile = fattn_splitkv_rows_per_tile(std::min(p.R, 64));
     p.n_row_tiles = (p.R + pl.rows_per_tile - 1) / pl.rows_per_tile;
@@ -265,19 +301,20 @@ int make_plan(const al_fattn_args * a, int n_cu, Plan * out) {
 }  // namespace
 
 extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
-    int n_cu = 0;
-    if (al_device_cu_count(&n_cu) != AL_OK) return 0;
+    int n_cu = 0, lds = 0;
+    if (al_device_cu_count(&n_cu) != AL_OK || al_device_lds_per_block(&lds) != AL_OK) return 0;
     Plan pl;
-    if (make_plan(a, n_cu, &pl) != AL_OK) return 0;
+    if (make_plan(a, n_cu, lds, &pl) != AL_OK) return 0;
     return pl.counters_bytes + pl.part_bytes;
 }
 
 extern "C" int al_fattn_f16(const al_fattn_args * a) {
-    int n_cu = 0;
+    int n_cu = 0, lds = 0;
     int rc = al_device_cu_count(&n_cu);
+    if (rc == AL_OK) rc = al_device_lds_per_block(&lds);
     if (rc != AL_OK) return rc;
     Plan pl;
-    rc = make_plan(a, n_cu, &pl);
+    rc = make_plan(a, n_cu, lds, &pl);
     if (rc != AL_OK) return rc;
     const size_t need = pl.counters_bytes + pl.part_bytes;
     if (need) {
@@ -293,7 +330,8 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
         pl.p.counters = (unsigned *) ws;
         pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
     }
-    const hipError_t e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream);
+    const hipError_t e = pl.prefill ? fattn_prefill_launch(pl.p, (hipStream_t) a->stream)
+                                    : fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream);
     if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
     return AL_OK;
 }

@@ -38,6 +38,12 @@ int fattn_splitkv_rows_per_tile(int R);
 int fattn_splitkv_waves(int rows_per_tile);
 hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
 
+// Prefill kernel: 64-row tiles, implicit masks only, one workgroup per
+// (kv head, row tile, stream); needs fattn_prefill_lds_bytes() of LDS.
+hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream);
+size_t fattn_prefill_lds_bytes();
+constexpr int kFattnPrefillRows = 64;
+
 // Floats of one split-KV merge record row (O[128], m, l, pad).
 constexpr int kFattnRecordStride = 132;
 // At most kFattnMaxSplit splits per row tile; one merge level.

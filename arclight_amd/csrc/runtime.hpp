@@ -10,4 +10,5 @@ void al_clear_error();
 
 // Per-device state, created on first use with the device current.
 int al_device_cu_count(int * n_cu);
+int al_device_lds_per_block(int * bytes);
 int al_device_error_flag(int ** flag);   // int[2]: {set, first bad index}

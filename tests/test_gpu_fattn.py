@@ -238,3 +238,28 @@ def test_shapes_alternating_on_one_workspace(gpu):
     cnt = np.empty(65536, dtype=np.uint32)
     ws.download(cnt)
     assert not cnt.any(), "arrival counters not left at zero"
+
+
+@pytest.mark.parametrize("pos0", [0, 1536])
+def test_prefill_kernel_chunk512_qwen3_4b(gpu, pos0):
+    # 512-token chunk of a 2048-token causal prefill (Hq 32, Hkv 8): enough
+    # 64-row tiles to take the dedicated prefill kernel
+    n_kv = 2048
+    q, k, v = O.make_inputs(500 + pos0, T=512, Hq=32, Hkv=8, n_kv=n_kv)
+    _check(f"prefill chunk 512 pos0 {pos0}", q, k, v, scale=SCALE, kv_len=pos0 + 512, causal_pos0=pos0)
+
+
+def test_prefill_kernel_gqa8_noncausal_sinks_softcap(gpu):
+    rng = np.random.default_rng(8)
+    q, k, v = O.make_inputs(600, T=256, Hq=64, Hkv=8, n_kv=1000)
+    _check("prefill gqa8 chunk 256 causal", q, k, v, scale=SCALE, kv_len=1000, causal_pos0=700)
+    _check("prefill gqa8 non-causal kv_len 777", q, k, v, scale=SCALE, kv_len=777)
+    sinks = rng.standard_normal(64).astype(np.float32)
+    _check("prefill gqa8 sinks + softcap", q, k, v, None, sinks, scale=SCALE * 3, logit_softcap=4.0,
+           kv_len=1000, causal_pos0=744)
+
+
+def test_prefill_kernel_streams_ragged(gpu):
+    # two streams, rows not a multiple of 64, cells not a multiple of 32
+    q, k, v = O.make_inputs(601, B=2, T=510, Hq=16, Hkv=4, n_kv=1111)
+    _check("prefill B=2 T=510 ragged", q, k, v, scale=SCALE, kv_len=1100, causal_pos0=590)
