@@ -49,6 +49,7 @@ SIGNATURES = {
     "al_util_fill_randn_f32": (_I, [_VP, _U64, _U64, _U64, _VP]),
     "al_util_fill_randn_f16": (_I, [_VP, _U64, _U64, _U64, _VP]),
     "al_util_f32_to_f16": (_I, [_VP, _VP, _U64, _VP]),
+    "al_util_copy_kernel": (_I, [_VP, _VP, _U64, _VP]),
 }
 
 _lib = None

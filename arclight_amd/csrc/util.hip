@@ -126,6 +126,12 @@ __global__ void f32_to_f16_kernel(_Float16 * dst, const float * src, uint64_t n)
         dst[i] = (_Float16) src[i];
 }
 
+// 16-byte vector copy, grid-stride; n16 = number of 16-byte words
+__global__ void copy16_kernel(uint4 * __restrict__ dst, const uint4 * __restrict__ src, uint64_t n16) {
+    for (uint64_t i = blockIdx.x * (uint64_t) blockDim.x + threadIdx.x; i < n16; i += (uint64_t) gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 unsigned grid_for(uint64_t n) {
     const uint64_t b = (n + 255) / 256;
     return (unsigned) (b < 8192 ? (b ? b : 1) : 8192);
@@ -151,5 +157,17 @@ extern "C" int al_util_f32_to_f16(uint16_t * dst, const float * src, uint64_t n,
     if (!n) return AL_OK;
     hipLaunchKernelGGL(f32_to_f16_kernel, dim3(grid_for(n)), dim3(256), 0, (hipStream_t) stream, (_Float16 *) dst, src, n);
     AL_HIP(hipGetLastError(), "f32_to_f16 launch");
+    return AL_OK;
+}
+
+extern "C" int al_util_copy_kernel(void * dst, const void * src, uint64_t bytes, void * stream) {
+    if (bytes % 16 || ((uintptr_t) dst | (uintptr_t) src) % 16)
+        return al_fail(AL_ERR_INVALID, "al_util_copy_kernel: bytes and pointers must be 16-byte aligned");
+    if (!bytes) return AL_OK;
+    const uint64_t n16 = bytes / 16;
+    const uint64_t blocks = (n16 + 255) / 256;
+    hipLaunchKernelGGL(copy16_kernel, dim3((unsigned) (blocks < 16384 ? blocks : 16384)), dim3(256), 0,
+                       (hipStream_t) stream, (uint4 *) dst, (const uint4 *) src, n16);
+    AL_HIP(hipGetLastError(), "copy16 launch");
     return AL_OK;
 }

@@ -30,6 +30,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0       # MI355X dense f16 MFMA, TFLOP/s
+DECODE_KERNEL = "fattn_splitkv_kernel<1, 8, true, false>"   # the launch decode at q_len 1 takes
 
 
 def parse():
@@ -107,27 +108,6 @@ def time_graph(lib, stream, arg_list, steps, warmup):
     return ms
 
 
-def time_per_launch(lib, stream, arg_list, reps):
-    """Average kernel duration from an event pair around every launch."""
-    from arclight_amd import device
-    n = len(arg_list) * reps
-    ev = [(device.Event(), device.Event()) for _ in range(n)]
-    f = lib.al_fattn_f16
-    i = 0
-    device.synchronize()
-    for _ in range(reps):
-        for a in arg_list:
-            ev[i][0].record(stream)
-            f(ctypes.byref(a))
-            ev[i][1].record(stream)
-            i += 1
-    stream.synchronize()
-    d = [s.elapsed_ms(e) for s, e in ev]
-    for s, e in ev:
-        s.destroy(); e.destroy()
-    return float(np.mean(d)), float(np.median(d))
-
-
 def decode_bytes(ctx, Hq, Hkv, D, T=1):
     return 2 * ctx * Hkv * D * 2 + 2 * T * Hq * D * 4
 
@@ -145,15 +125,14 @@ def bench_decode(lib, stream, a):
     lay = Layers(L, 1, Hq, Hkv, D, ctx, a.seed)
     args = [lay.args(l, stream, scale, kv_len=ctx) for l in range(L)]
     ms = time_graph(lib, stream, args, a.steps, a.warmup)
-    k_mean, k_med = time_per_launch(lib, stream, args, max(2, a.steps // 4))
     byts = decode_bytes(ctx, Hq, Hkv, D)
+    # the timed region is L back-to-back launches of the decode kernel on this
+    # stream, so its average launch duration is ms / L
     return {
         "ms_per_step": ms,
         "bytes_per_layer": byts,
         "gbs": byts * L / (ms * 1e-3) / 1e9,
-        "kernel_ms_mean": k_mean,
-        "kernel_ms_median": k_med,
-        "kernel_gbs": byts / (k_mean * 1e-3) / 1e9,
+        "kernel_ms_mean": ms / L,
     }
 
 
@@ -174,10 +153,9 @@ def bench_prefill(lib, stream, a):
                                      c * chunk * Hq * D * 4, abi.DST_AXES)
             args.append(lay.args(l, stream, scale, kv_len=chunk * (c + 1), causal_pos0=chunk * c, q=qv, dst=dv))
     ms = time_graph(lib, stream, args, max(1, a.steps // 2), max(1, a.warmup))
-    k_mean, _ = time_per_launch(lib, stream, args, 1)
     fl = prefill_flops(T_total, chunk, Hq, D)
     return {"ms_per_step": ms, "flops_per_layer": fl, "tflops": fl * L / (ms * 1e-3) / 1e12,
-            "kernel_ms_mean": k_mean}
+            "kernel_ms_mean": ms / len(args)}
 
 
 def bench_copy(stream, nbytes=1 << 30):
@@ -188,11 +166,11 @@ def bench_copy(stream, nbytes=1 << 30):
     call("al_util_memset", a_.ptr, 1, nbytes)
     e0, e1 = device.Event(), device.Event()
     for _ in range(2):
-        call("al_util_memcpy_d2d", b_.ptr, a_.ptr, nbytes, stream.handle)
+        call("al_util_copy_kernel", b_.ptr, a_.ptr, nbytes, stream.handle)
     e0.record(stream)
     reps = 10
     for _ in range(reps):
-        call("al_util_memcpy_d2d", b_.ptr, a_.ptr, nbytes, stream.handle)
+        call("al_util_copy_kernel", b_.ptr, a_.ptr, nbytes, stream.handle)
     e1.record(stream)
     e1.synchronize()
     ms = e0.elapsed_ms(e1) / reps
@@ -225,12 +203,18 @@ def cpu_baseline(a):
                       f"{el:.1f} s, {per * 1e3:.1f} ms/layer"}
 
 
-def load_traffic():
+def load_traffic(kernel, ctx):
+    """HBM bytes per decode launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (scaled by the copy-kernel calibration), if they were
+    taken for this kernel and context; else None."""
     p = os.path.join(ROOT, "profiles", "decode_traffic.json")
-    if os.path.exists(p):
-        with open(p) as f:
-            return json.load(f)
-    return None
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        t = json.load(f)
+    if t.get("kernel") != kernel or t.get("ctx") != ctx:
+        return None
+    return t.get("bytes_per_launch")
 
 
 def main():
@@ -264,7 +248,8 @@ def main():
     if cpu:
         print(f"[bench] cpu {cpu}", file=sys.stderr, flush=True)
 
-    traffic = load_traffic()
+    achieved = dec["bytes_per_layer"] / (dec["kernel_ms_mean"] * 1e-3) / 1e9
+    traffic = load_traffic(DECODE_KERNEL, a.ctx)
     out = {
         "metric": "decode-attn KV GB/s (% HBM peak) + prefill-attn TFLOP/s, Qwen3-4B shape",
         "value": round(dec["gbs"], 1),
@@ -282,10 +267,10 @@ def main():
                                f"context {a.ctx}, {a.layers} layers back to back, one cache slice per layer",
                    "parallelism": "single GPU"},
         "hbm_peak_frac": round(dec["gbs"] / HBM_PEAK_GBS, 4),
-        "roofline": {"bound": "hbm", "achieved": round(dec["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(dec["kernel_gbs"] / HBM_PEAK_GBS, 4),
-                     "traffic": traffic.get("bytes_per_launch") if traffic else None,
-                     "kernel": "fattn_splitkv_kernel<1,true>",
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": traffic,
+                     "kernel": DECODE_KERNEL,
                      "kernel_us_mean": round(dec["kernel_ms_mean"] * 1e3, 2),
                      "algorithmic_bytes_per_launch": dec["bytes_per_layer"]},
         "prefill": None if not pre else {

@@ -58,6 +58,11 @@ int al_util_fill_randn_f16(uint16_t * dst, uint64_t n, uint64_t seed, uint64_t o
  * KV-write rounding of the reference, nnml/include/ops.h:299-323). */
 int al_util_f32_to_f16(uint16_t * dst, const float * src, uint64_t n, void * stream);
 
+/* Plain device copy by a 16-byte vector kernel (bytes and both pointers
+ * 16-byte aligned): a kernel of known traffic, 2 * bytes, that calibrates
+ * hardware byte counters. */
+int al_util_copy_kernel(void * dst, const void * src, uint64_t bytes, void * stream);
+
 #ifdef __cplusplus
 }
 #endif
