@@ -145,9 +145,13 @@ static int library_workspace(size_t bytes, void ** ptr) {
 
 namespace {
 
+enum Kernel { kSplitKV, kPrefill, kDecode };
+
 struct Plan {
     FattnParams p;
-    bool prefill = false;
+    Kernel kernel = kSplitKV;
+    int waves = 2;                  // decode kernel: wavefronts per workgroup
+    int stages = 2;                 // decode kernel: LDS stage buffers
     int rows_per_tile = 16;
     size_t counters_bytes = 0;
     size_t part_bytes = 0;
@@ -164,12 +168,54 @@ bool prefer_prefill() {
     return v;
 }
 
+int env_int(const char * name, int dflt) {
+    const char * s = getenv(name);
+    const int x = s ? atoi(s) : 0;
+    return x > 0 ? x : dflt;
+}
+
 int wgs_per_cu() {
-    static int v = [] {
-        const char * s = getenv("AL_SPLITKV_WGS_PER_CU");
-        const int x = s ? atoi(s) : 0;
-        return x > 0 ? x : 2;
+    static int v = env_int("AL_SPLITKV_WGS_PER_CU", 2);
+    return v;
+}
+
+// AL_FATTN_DECODE=0 keeps decode calls on the split-KV kernel.
+bool prefer_decode() {
+    static bool v = [] {
+        const char * s = getenv("AL_FATTN_DECODE");
+        return !(s && s[0] == '0');
     }();
+    return v;
+}
+
+// Decode kernel sizing: workgroups per CU to aim for, and the fewest 16-cell
+// stages a split may hold.
+int decode_wgs_per_cu() {
+    static int v = env_int("AL_DECODE_WGS_PER_CU", 4);
+    return v;
+}
+// Decode kernel shape: wavefronts per workgroup (AL_DECODE_WAVES) and LDS
+// stage buffers per wave (AL_DECODE_STAGES); combinations without a kernel
+// fall back to 2 x 3, the fastest measured at 32K context (fewer, deeper
+// streams per CU beat more of them).
+int decode_waves() {
+    static int v = env_int("AL_DECODE_WAVES", 2);
+    return v;
+}
+int decode_stages() {
+    static int v = env_int("AL_DECODE_STAGES", 3);
+    return v;
+}
+// AL_DECODE_INTERLEAVE=0: each split takes a contiguous cell range.
+bool decode_interleave() {
+    static bool v = [] {
+        const char * s = getenv("AL_DECODE_INTERLEAVE");
+        return !(s && s[0] == '0');
+    }();
+    return v;
+}
+int decode_min_stages() {
+    static int v = env_int("AL_DECODE_MIN_STAGES", 2);
     return v;
 }
 
@@ -240,6 +286,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     if (m.data) {
         p.mask = (const char *) m.data; p.m_nb1 = m.nb[1]; p.m_nb2 = m.nb[2]; p.m_nb3 = m.nb[3];
         p.m_ne0 = (int32_t) std::min<int64_t>(m.ne[0], INT32_MAX); p.m_ne2 = (int32_t) m.ne[2]; p.m_ne3 = (int32_t) m.ne[3];
+        const uint64_t slice = (uint64_t) (m.ne[2] - 1) * m.nb[2] + (uint64_t) (m.ne[1] - 1) * m.nb[1] + (uint64_t) m.ne[0] * 2;
+        p.m_slice_bytes = (uint32_t) std::min<uint64_t>(slice, INT32_MAX);
     }
     p.sinks = (const float *) s.data;
     p.dst = (char *) d.data; p.dst_nb1 = d.nb[1];
@@ -262,11 +310,54 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
     if (!m.data && p.R > 32 && prefill_tiles * Hkv * B >= n_cu && lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
         prefer_prefill()) {
-        pl.prefill = true;
+        pl.kernel = kPrefill;
         pl.rows_per_tile = kFattnPrefillRows;
         p.n_row_tiles = (int32_t) prefill_tiles;
         p.n_split = 1;
         p.cells_per_split = 0;
+        *out = pl;
+        return AL_OK;
+    }
+
+    // Up to 16 rows per kv head: the decode kernel, when its LDS rings fit
+    // and a head's K/V view is addressable with 32-bit offsets.
+    int dwaves = decode_waves(), stages = decode_stages();
+    if (!fattn_decode_config_ok(dwaves, stages)) {
+        dwaves = 2;
+        stages = 3;
+    }
+    const size_t decode_lds = fattn_decode_lds_bytes(dwaves, stages, m.data != nullptr);
+    const bool mask_ok = !m.data || (p.m_slice_bytes < INT32_MAX && aligned16(m.data) && m.nb[1] % 16 == 0 &&
+                                     m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
+    const int64_t decode_units = Hkv * B;
+    if (p.R <= 16 && prefer_decode() && (size_t) lds_per_block >= decode_lds && mask_ok &&
+        decode_units * sizeof(unsigned) <= kFattnCounterBytes &&
+        (uint64_t) (n_kv + 16) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
+        (uint64_t) (n_kv + 16) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX) {
+        pl.kernel = kDecode;
+        pl.waves = dwaves;
+        pl.stages = stages;
+        pl.rows_per_tile = 16;
+        p.n_row_tiles = 1;
+        int64_t extent = p.kv_hi;
+        if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
+        extent = std::max<int64_t>(extent, 0);
+        const int64_t nst = std::max<int64_t>(1, (extent + 15) / 16);   // 16-cell stages
+        // workgroups resident per CU by LDS (160 KiB per CU on gfx950)
+        const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (int64_t) (160 << 10) / (int64_t) decode_lds));
+        const int64_t target = (int64_t) n_cu * std::min<int64_t>(per_cu, decode_wgs_per_cu());
+        int64_t n_split = (target + decode_units - 1) / decode_units;
+        // every wave of a split gets at least decode_min_stages() stages
+        n_split = std::min<int64_t>(n_split, std::max<int64_t>(1, nst / (dwaves * decode_min_stages())));
+        n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, kFattnMaxSplit));
+        const int64_t cps = (nst + n_split - 1) / n_split;
+        p.cells_per_split = (int32_t) (cps * 16);
+        p.n_split = (int32_t) ((nst + cps - 1) / cps);
+        p.interleave = decode_interleave() ? 1 : 0;
+        if (p.n_split > 1) {
+            pl.counters_bytes = kFattnCounterBytes;
+            pl.part_bytes = (size_t) decode_units * p.n_split * 16 * kFattnRecordStride * sizeof(float);
+        }
         *out = pl;
         return AL_OK;
     }
@@ -330,8 +421,12 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
         pl.p.counters = (unsigned *) ws;
         pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
     }
-    const hipError_t e = pl.prefill ? fattn_prefill_launch(pl.p, (hipStream_t) a->stream)
-                                    : fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream);
+    hipError_t e;
+    switch (pl.kernel) {
+        case kPrefill: e = fattn_prefill_launch(pl.p, (hipStream_t) a->stream); break;
+        case kDecode:  e = fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream); break;
+        default:       e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
+    }
     if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
     return AL_OK;
 }

@@ -1,0 +1,468 @@
+// Decode (and short speculative-verify) attention for gfx950: up to 16 query
+// rows per kv head, K/V streamed through LDS a whole cell range at a time.
+// Semantics as nnml_compute_forward_flash_attn_ext_f16
+// (nnml/src/ops/arm/arm.cpp:2196-2433), numerics as fattn_splitkv.hip.
+//
+// Work decomposition. A workgroup owns one kv head of one cell range (a
+// split) of one stream and keeps up to 16 query rows of the head's group
+// (row r -> token r / G, head kvh*G + r % G). Its WS wavefronts take the
+// range's 16-cell stages in turn (wave ws: stages ws, ws + WS, ...), each
+// with a private ring of NB LDS stage buffers, so the waves never wait for
+// each other until the end. The 1-D grid runs split fastest.
+//
+// Memory path. A stage is the head's 16 K rows and 16 V rows (4 KiB each),
+// moved by LDS-DMA buffer loads of 1 KiB per instruction (4 cells x 256 B),
+// 8 per stage, so a wave has NB - 1 stages (up to 24 KiB) in flight while it
+// computes one. Inside a 256-byte row the 16-byte granules are XOR-swizzled
+// by the cell index (granule j of cell c sits at slot j ^ c), which makes
+// both operand reads below free of LDS bank conflicts. The DMA is issued by
+// inline assembly, so the compiler neither counts it nor makes LDS reads of
+// the current stage wait for the stages still in flight; each wave waits
+// for its own stage (s_waitcnt vmcnt).
+//
+// Per wave and stage:
+//   S^T[16 cells x 16 rows]  = K Q^T      4 MFMA 16x16x32 (K rows read as
+//                                         A operands, one granule per lane)
+//   O^T[128 dims x 16 rows] += V^T P^T    8 MFMA 16x16x16 (V^T operands read
+//                                         by ds_read_b64_tr_b16, which
+//                                         transposes 4 cells x 16 dims per
+//                                         16-lane group on the way out)
+// P^T comes from S^T in place: both keep cell 4g+i, row n in lane 16g+n.
+// O^T lane 16g+n holds dims 16mb + 4g + i of row n (mb = 0..7).
+//
+// Merge. The WS waves merge their online-softmax states through LDS. With
+// one split the workgroup then writes dst; otherwise it publishes one
+// record per row with device-coherent stores, bumps the arrival counter of
+// its (stream, kv head), and the last workgroup to arrive merges the at most
+// 32 splits (all loads in flight, fixed order, so results are
+// bit-reproducible) and writes dst.
+
+#include "fattn_tile.hpp"
+
+namespace {
+
+using namespace fattn;
+
+constexpr int kSC = 16;                                   // cells per stage
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8; all-ones = no wait)
+constexpr int vmcnt_imm(int v) { return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+__device__ __forceinline__ floatx4 mfma_16x16x16(half4 a, half4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane s supplies 8 bytes (4 f16)
+// that form elements 4(s%4)..4(s%4)+3 of row s/4 of a 4 x 16 matrix; lane i
+// receives column i, i.e. element i%4 of the 8 bytes of lanes i/4, 4+i/4,
+// 8+i/4 and 12+i/4.
+__device__ __forceinline__ half4 lds_read_tr16(const char * p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v *) p);
+    return __builtin_bit_cast(half4, r);
+}
+
+__device__ __forceinline__ void mem_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// Raw buffer descriptor (the layout make_rsrc builds) for the inline DMA.
+__device__ __forceinline__ int4v raw_desc(const void * base, uint32_t bytes) {
+    const uint64_t a = (uint64_t) base;
+    return int4v{(int) (uint32_t) a, (int) (uint32_t) (a >> 32), (int) bytes, 0x00020000};
+}
+
+// One LDS-DMA load: 16 bytes per lane from desc + voff into LDS at
+// lds_base + 16 * lane. M0 carries the LDS address; nothing else in these
+// kernels uses M0 (the compiler warns that a clobbered reserved register is
+// not preserved, which is the intent here).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const int4v desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(desc), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) char *) p;
+}
+
+// Waits until at most `later` stages of PER memory operations each are still
+// outstanding (the stages issued after the one about to be read).
+template <int NB, int PER>
+__device__ __forceinline__ void wait_stage(int later) {
+    mem_barrier();
+    if constexpr (NB >= 4) {
+        if (later >= 2) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); mem_barrier(); return; }
+    }
+    if constexpr (NB >= 3) {
+        if (later >= 1) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); mem_barrier(); return; }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    mem_barrier();
+}
+
+template <int WS, int NB, bool HAS_MASK>
+__global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p) {
+    static_assert(WS == 2 || WS == 4 || WS == 8, "the wave merge is a binary tree");
+    constexpr int PER = 8 + (HAS_MASK ? 1 : 0);           // DMA loads per stage
+    constexpr int STAGE = 8192 + (HAS_MASK ? 1024 : 0);   // K rows, V rows, mask rows
+    constexpr int REC = 16 * kRowStride;                  // floats of one 16-row state record
+    static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
+    __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
+    __shared__ int s_last;
+
+    const int lane = threadIdx.x & 63;
+    const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4;
+    const int n = lane & 15;
+
+    int id = blockIdx.x;
+    const int split = id % p.n_split;
+    id /= p.n_split;
+    const int kvh = id % p.Hkv;
+    const int b = id / p.Hkv;
+    const int unit = b * p.Hkv + kvh;
+    const int rows_here = min(16, p.R);
+    const int t_last = (rows_here - 1) / p.G;
+
+    int hi = p.kv_hi;
+    if (p.causal_pos0 >= 0) hi = (int) min((int64_t) hi, p.causal_pos0 + t_last + 1);
+    // Stages of this workgroup: with interleave, global 16-cell stages
+    // split, split + n_split, ... of [0, hi) (all splits of a head sweep the
+    // cache together); else the contiguous range [c_begin, c_end). Wave ws
+    // takes the workgroup's stages ws, ws + WS, ...
+    const int c_begin = p.interleave ? 16 * split : split * p.cells_per_split;
+    const int c_end = p.interleave ? hi : min(c_begin + p.cells_per_split, hi);
+    const int sstride = p.interleave ? kSC * p.n_split : kSC;              // cells between the workgroup's stages
+    const int ns = c_end > c_begin ? (c_end - c_begin + sstride - 1) / sstride : 0;
+    const int my_ns = ns > ws ? (ns - ws + WS - 1) / WS : 0;
+
+    // K/V rows of this stream and head (loads past the end read 0)
+    const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
+    const char * kbase = p.k + (int64_t) (b / p.rk3) * p.k_nb3 + (int64_t) kvh * p.k_nb2;
+    const char * vbase = p.v + (int64_t) (b / p.rv3) * p.v_nb3 + (int64_t) kvh * p.v_nb2;
+    const int4v kd = raw_desc(kbase, (uint32_t) (p.n_kv - 1) * k_nb1 + 256);
+    const int4v vd = raw_desc(vbase, (uint32_t) (p.n_kv - 1) * v_nb1 + 256);
+
+    // DMA block i (0..3 K, 4..7 V) of a stage: LDS granule 64(i & 3) + lane
+    // is cell 4(i & 3) + lane / 16, slot lane % 16, holding the global
+    // granule slot ^ cell.
+    const int dcell = lane >> 4;                           // + 4 (i & 3)
+    const uint32_t dk = (uint32_t) dcell * k_nb1, dv = (uint32_t) dcell * v_nb1;
+    uint32_t dj[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dj[i] = (uint32_t) (((lane & 15) ^ (4 * i + dcell)) * 16);
+    const uint32_t ring = lds_addr(&lds[ws][0][0]);
+
+    // this lane's query row: column n of the single row block
+    const int r = n;
+    const bool rvalid = r < rows_here;
+    const int tok = rvalid ? r / p.G : 0;
+    const int head = kvh * p.G + (rvalid ? r % p.G : 0);
+
+    // Mask rows (f16, cells along a row) also travel by DMA, one 1 KiB block
+    // per stage: lane l < 32 loads cells 8(l & 1)..+7 of row l >> 1 to LDS
+    // bytes 16 l (lanes 32..63 repeat lanes 0..31), from a buffer over the
+    // stream's mask slice; cells past a row read whatever follows, and are
+    // past the length limit anyway.
+    int4v md = {0, 0, 0, 0};
+    uint32_t msrc = 0;
+    if constexpr (HAS_MASK) {
+        md = raw_desc(p.mask + (int64_t) (b % p.m_ne3) * p.m_nb3, p.m_slice_bytes);
+        const int mrow = (lane >> 1) & 15;
+        const int mt_ = mrow < rows_here ? mrow / p.G : 0;
+        const int mh = kvh * p.G + (mrow < rows_here ? mrow % p.G : 0);
+        msrc = (uint32_t) ((int64_t) mt_ * p.m_nb1 + (int64_t) (mh % p.m_ne2) * p.m_nb2) + (uint32_t) ((lane & 1) * 16);
+    }
+
+    // This wave's j-th stage (cells c_begin + sstride (ws + j WS) ..) into ring slot u.
+    auto issue = [&](const int j, const int u) {
+        const uint32_t cs = (uint32_t) (c_begin + sstride * (ws + j * WS));
+        const uint32_t kofs = cs * k_nb1 + dk, vofs = cs * v_nb1 + dv;
+        const uint32_t base = ring + (uint32_t) (u * STAGE);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            dma16(kd, kofs + (uint32_t) (4 * i) * k_nb1 + dj[i], base + (uint32_t) (i * 1024));
+            dma16(vd, vofs + (uint32_t) (4 * i) * v_nb1 + dj[i], base + (uint32_t) (4096 + i * 1024));
+        }
+        if constexpr (HAS_MASK) dma16(md, msrc + cs * 2, base + 8192u);
+    };
+
+    // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
+    // (converted before the first DMA: the compiler does not count the DMA,
+    // so a wait for q after it would wait for every stage in flight)
+    half8 qf[4];
+    {
+        const float * qrow = (const float *) (p.q + (int64_t) b * p.q_nb3 + (int64_t) tok * p.q_nb1 +
+                                              (int64_t) head * p.q_nb2);
+        float4 qa[4], qb[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            qa[kb] = *(const float4 *) (qrow + 8 * (4 * kb + g));
+            qb[kb] = *(const float4 *) (qrow + 8 * (4 * kb + g) + 4);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) qf[kb] = rvalid ? to_half8(qa[kb], qb[kb]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    }
+    mem_barrier();
+#pragma unroll
+    for (int u = 0; u < NB - 1; ++u)
+        if (u < my_ns) issue(u, u);
+
+    float slope = 1.0f;
+    if (p.max_bias > 0.0f) {                                           // arm.cpp:2294
+        const uint32_t hq = (uint32_t) head;
+        slope = hq < p.n_head_log2 ? powf(p.m0, (float) (hq + 1)) : powf(p.m1, (float) (2 * (hq - p.n_head_log2) + 1));
+    }
+    const int lim = row_limit(p, hi, rvalid, tok);
+    const int lim_min = row_limit(p, hi, true, 0);
+
+    floatx4 o[8];
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) o[mb] = floatx4{0, 0, 0, 0};
+    float m_run = -AL_INF;
+    float l_run = 0.0f;
+
+    // LDS read offsets of this lane within a stage
+    const int kread = n * 256;                                          // K row of cell n
+    const int vcell = 4 * g + (n >> 2);                                 // V cell this lane supplies
+    const int vread = 4096 + vcell * 256 + (n & 1) * 8;
+
+    for (int j0 = 0; j0 < my_ns; j0 += NB) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int j = j0 + u;
+            if (j >= my_ns) break;
+            // this stage landed (own DMA); slot (u + NB - 1) % NB was read
+            // last iteration, so the stage NB - 1 ahead may fill it now
+            wait_stage<NB, PER>(min(NB - 2, my_ns - 1 - j));
+            if (j + NB - 1 < my_ns) issue(j + NB - 1, (u + NB - 1) % NB);
+            mem_barrier();
+            const char * st = &lds[ws][u][0];
+            const int cs = c_begin + sstride * (ws + j * WS);
+            u32x4 kf[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) kf[kb] = *(const u32x4 *) (st + kread + (((4 * kb + g) ^ n) << 4));
+            half4 vt[8];
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) vt[mb] = lds_read_tr16(st + vread + (((2 * mb + ((n & 3) >> 1)) ^ vcell) << 4));
+            uint2 mk = {0, 0};
+            if constexpr (HAS_MASK) mk = *(const uint2 *) (st + 8192 + 32 * n + 8 * g);
+
+            // S^T: cells 4g+i of row n
+            floatx4 sc = {0, 0, 0, 0};
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) sc = mfma_16x16x32(as_half8(kf[kb]), qf[kb], sc);
+            sc *= p.scale;
+            if (p.softcap != 0.0f) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) sc[i] = p.softcap * tanhf(sc[i]);
+            }
+            const bool full = !HAS_MASK && cs + kSC - 1 <= lim_min;
+            bool vis_any[4] = {true, true, true, true};
+            if (!full) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    bool vis = cs + 4 * g + i <= lim;
+                    float x = sc[i];
+                    if constexpr (HAS_MASK) {
+                        const uint32_t w = i < 2 ? mk.x : mk.y;
+                        const float mv = slope * f16_bits_to_float((uint16_t) (w >> (16 * (i & 1))));
+                        vis = vis && (mv != -AL_INF);
+                        x += mv;
+                    }
+                    sc[i] = vis ? x : -AL_INF;
+                    vis_any[i] = vis;
+                }
+            }
+            const float mt = colmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+            if (__any(mt > m_run + kTau)) {
+                const bool grow = mt > m_run + kTau;
+                const float mn = grow ? mt : m_run;
+                const float alpha = grow ? exp_fast(m_run - mn) : 1.0f;
+                l_run *= alpha;
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) o[mb] *= alpha;
+                m_run = mn;
+            }
+            const float mu = (m_run == -AL_INF) ? 0.0f : m_run;
+            half4 pf;
+            float ps = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pr = exp_fast(sc[i] - mu);
+                ps += pr;
+                pf[i] = (_Float16) pr;
+            }
+            l_run += ps;
+            if (!full) {
+                // cells masked for every row contribute exact zeros, whatever their V holds
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint64_t bal = __ballot(vis_any[i]);
+                    if (((bal >> (16 * g)) & 0xffffull) == 0) {
+#pragma unroll
+                        for (int mb = 0; mb < 8; ++mb) vt[mb][i] = (_Float16) 0.0f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) o[mb] = mfma_16x16x16(vt[mb], pf, o[mb]);
+        }
+    }
+    l_run = colsum4(l_run);
+
+    // merge the WS waves through LDS records [slot][row][132] (the rings are
+    // free once every wave is past its loop)
+    if constexpr (WS > 1) {
+        float * recs = (float *) &lds[0][0][0];
+#pragma unroll
+        for (int span = WS / 2; span >= 1; span /= 2) {
+            __syncthreads();
+            if (ws >= span && ws < 2 * span) {
+                float * rec = recs + (ws - span) * REC + n * kRowStride;
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) *(float4 *) (rec + 16 * mb + 4 * g) = float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]};
+                if (g == 0) *(float2 *) (rec + 128) = float2{m_run, l_run};
+            }
+            __syncthreads();
+            if (ws < span) {
+                const float * rec = recs + ws * REC + n * kRowStride;
+                const float2 ml = *(const float2 *) (rec + 128);
+                const float mn = fmaxf(m_run, ml.x);
+                const float mu = (mn == -AL_INF) ? 0.0f : mn;
+                const float wa = exp_fast(m_run - mu);
+                const float wb = exp_fast(ml.x - mu);
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) {
+                    const float4 x = *(const float4 *) (rec + 16 * mb + 4 * g);
+                    o[mb][0] = o[mb][0] * wa + x.x * wb;
+                    o[mb][1] = o[mb][1] * wa + x.y * wb;
+                    o[mb][2] = o[mb][2] * wa + x.z * wb;
+                    o[mb][3] = o[mb][3] * wa + x.w * wb;
+                }
+                l_run = l_run * wa + ml.y * wb;
+                m_run = mn;
+            }
+        }
+    }
+
+    if (p.n_split == 1) {
+        if (ws == 0 && rvalid) {
+            float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok) * p.Hq + head) * p.dst_nb1);
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb)
+                *(float4 *) (out + 16 * mb + 4 * g) =
+                    finalize4(float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]}, m_run, l_run, p.sinks, head);
+        }
+        return;
+    }
+
+    // publish this split's record: [unit][split][row][132]
+    constexpr uint32_t RS = REC * 4;                                   // bytes of one split's record
+    const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * REC, RS * (uint32_t) p.n_split);
+    if (ws == 0 && rvalid) {
+        const uint32_t row = (uint32_t) split * RS + (uint32_t) (r * kRowStride * 4);
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb)
+            buf_store16_dev(float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]}, pr, row + (16 * mb + 4 * g) * 4);
+        if (g == 0) buf_store8_dev(float2{m_run, l_run}, pr, row + 128 * 4);
+    }
+    complete_wave_memops();
+    __syncthreads();
+    unsigned * cnt = p.counters + unit;
+    if (threadIdx.x == 0) s_last = (add_agent(cnt, 1u) == (unsigned) (p.n_split - 1));
+    __syncthreads();
+    if (!s_last) return;
+    order_after_counter();
+    if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
+
+    // Last workgroup: two adjacent lanes per (row, 4 dims), each taking 16
+    // of the at most 32 splits with all their loads in flight, then
+    // combining with its partner (split half 0 first, on both lanes).
+    constexpr int kHalf = kMaxSplit / 2;
+    for (int idx = threadIdx.x; idx < rows_here * 64; idx += WS * 64) {
+        const int half = idx & 1;
+        const int d4 = (idx >> 1) & 31;
+        const int rr = idx >> 6;
+        float2 ml[kHalf];
+        float4 ov[kHalf];
+#pragma unroll
+        for (int j = 0; j < kHalf; ++j) {
+            const int sp = half * kHalf + j;
+            if (sp < p.n_split) {
+                const uint32_t row = (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4);
+                ml[j] = buf_load8_dev(pr, row + 128 * 4);
+                ov[j] = buf_load16_dev(pr, row + d4 * 16);
+            } else {
+                ml[j] = float2{-AL_INF, 0.0f};
+                ov[j] = float4{0, 0, 0, 0};
+            }
+        }
+        float Mh = ml[0].x;
+#pragma unroll
+        for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[j].x);
+        const float M = fmaxf(Mh, __shfl_xor(Mh, 1));
+        const float Mu = (M == -AL_INF) ? 0.0f : M;
+        float Lh = 0.0f;
+        float4 ah = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < kHalf; ++j) {
+            const float w = exp_fast(ml[j].x - Mu);
+            Lh += w * ml[j].y;
+            ah.x += w * ov[j].x; ah.y += w * ov[j].y; ah.z += w * ov[j].z; ah.w += w * ov[j].w;
+        }
+        const float Lo = __shfl_xor(Lh, 1);
+        const float4 ao = {__shfl_xor(ah.x, 1), __shfl_xor(ah.y, 1), __shfl_xor(ah.z, 1), __shfl_xor(ah.w, 1)};
+        if (half == 0) {
+            const float L = Lh + Lo;
+            const float4 acc = {ah.x + ao.x, ah.y + ao.y, ah.z + ao.z, ah.w + ao.w};
+            const int t = rr / p.G;
+            const int hq = kvh * p.G + rr % p.G;
+            float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
+            *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
+        }
+    }
+}
+
+template <int WS, int NB>
+hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
+    const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
+    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true>), grid, dim3(WS * 64), 0, stream, p);
+    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false>), grid, dim3(WS * 64), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool fattn_decode_config_ok(int waves, int stages) {
+    switch (waves * 10 + stages) {
+        case 23: case 24: case 43: case 44: case 82: return true;
+        default: return false;
+    }
+}
+
+size_t fattn_decode_lds_bytes(int waves, int stages, bool mask) {
+    return (size_t) waves * stages * (8192 + (mask ? 1024 : 0));
+}
+
+hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream) {
+    switch (waves * 10 + stages) {
+        case 23: return launch_cfg<2, 3>(p, stream);
+        case 24: return launch_cfg<2, 4>(p, stream);
+        case 43: return launch_cfg<4, 3>(p, stream);
+        case 44: return launch_cfg<4, 4>(p, stream);
+        case 82: return launch_cfg<8, 2>(p, stream);
+        default: return hipErrorInvalidValue;
+    }
+}

@@ -12,6 +12,7 @@ struct FattnParams {
     const char * v;     int64_t v_nb1, v_nb2, v_nb3;     // f16 [D, n_kv, Hkv, Bv]
     const char * mask;  int64_t m_nb1, m_nb2, m_nb3;     // f16 [m_ne0, rows, m_ne2, m_ne3] or null
     int32_t m_ne0, m_ne2, m_ne3;
+    uint32_t m_slice_bytes;                              // bytes of one mask stream slice (dims 0..2), clamped
     const float * sinks;                                 // f32 [Hq] or null
     char * dst;         int64_t dst_nb1;                 // f32 rows (i3*T + i1)*Hq + i2
 
@@ -28,6 +29,7 @@ struct FattnParams {
     int32_t n_row_tiles;
     int32_t n_split;
     int32_t cells_per_split;        // multiple of 32
+    int32_t interleave;             // decode kernel: splits take every n_split-th 16-cell stage
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
 };
@@ -43,6 +45,15 @@ hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStr
 hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream);
 size_t fattn_prefill_lds_bytes();
 constexpr int kFattnPrefillRows = 64;
+
+// Decode kernel: up to 16 query rows per kv head, one kv head per
+// workgroup, `waves` wavefronts each streaming 16-cell stages of K/V through
+// a private ring of `stages` LDS buffers; fattn_decode_config_ok tells which
+// combinations exist. At most kFattnMaxSplit splits per (stream, kv head);
+// arrival counters as the split-KV kernel's (one per stream x kv head).
+bool fattn_decode_config_ok(int waves, int stages);
+size_t fattn_decode_lds_bytes(int waves, int stages, bool mask);
+hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream);
 
 // Floats of one split-KV merge record row (O[128], m, l, pad).
 constexpr int kFattnRecordStride = 132;

@@ -102,14 +102,8 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
 
     // this wave's tiles: cells cb0 + it * 128
     constexpr int kStride = kPW * 32;
-    struct {
-        char * st[2];
-        int cb0, ntiles;
-    } c;
-    c.st[0] = lds[wave][0];
-    c.st[1] = lds[wave][1];
-    c.cb0 = wave * 32;
-    c.ntiles = c.cb0 < hi ? (hi - c.cb0 + kStride - 1) / kStride : 0;
+    const int cb0 = wave * 32;
+    const int ntiles = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
 
     int tok[kPRB];
     int head[kPRB];
@@ -148,24 +142,26 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
 #pragma unroll
         for (int d = 0; d < 8; ++d) o[rb][d] = floatx4{0, 0, 0, 0};
     }
-    if (c.ntiles > 0) dma_tile(c.st[0], p, kr, vr, c.cb0, g, n);
-    if (c.ntiles > 1) dma_tile(c.st[1], p, kr, vr, c.cb0 + kStride, g, n);
-    for (int it = 0; it < c.ntiles; ++it) {
-        char * cur = c.st[it & 1];
+    // (stage pointers are taken from the LDS array itself each time, so the
+    // compiler keeps them in the LDS address space: ds_read, not flat loads,
+    // which would count against vmcnt and wait for the DMA in flight)
+    if (ntiles > 0) dma_tile(lds[wave][0], p, kr, vr, cb0, g, n);
+    if (ntiles > 1) dma_tile(lds[wave][1], p, kr, vr, cb0 + kStride, g, n);
+    for (int it = 0; it < ntiles; ++it) {
         // this tile's 16 DMA loads are complete once at most the next tile's
         // 16 are outstanding
         mem_barrier();
-        if (it + 1 < c.ntiles) __builtin_amdgcn_s_waitcnt(kWaitVm16);
+        if (it + 1 < ntiles) __builtin_amdgcn_s_waitcnt(kWaitVm16);
         else __builtin_amdgcn_s_waitcnt(kWaitVm0);
         mem_barrier();
         Tile<kPRB> t;
-        read_k(t, cur, lane);
-        read_v(t, cur, lane);
+        read_k(t, lds[wave][it & 1], lane);
+        read_v(t, lds[wave][it & 1], lane);
         mem_barrier();
         __builtin_amdgcn_s_waitcnt(kWaitLgkm0);          // stage free again
         mem_barrier();
-        if (it + 2 < c.ntiles) dma_tile(cur, p, kr, vr, c.cb0 + (it + 2) * kStride, g, n);
-        process_tile<kPRB, false>(t, c.cb0 + it * kStride, p, g, lim, lim_min, slope, qf, o, m_run, l_run);
+        if (it + 2 < ntiles) dma_tile(lds[wave][it & 1], p, kr, vr, cb0 + (it + 2) * kStride, g, n);
+        process_tile<kPRB, false>(t, cb0 + it * kStride, p, g, lim, lim_min, slope, qf, o, m_run, l_run);
     }
 
 #pragma unroll

@@ -263,3 +263,20 @@ def test_prefill_kernel_streams_ragged(gpu):
     # two streams, rows not a multiple of 64, cells not a multiple of 32
     q, k, v = O.make_inputs(601, B=2, T=510, Hq=16, Hkv=4, n_kv=1111)
     _check("prefill B=2 T=510 ragged", q, k, v, scale=SCALE, kv_len=1100, causal_pos0=590)
+
+
+def test_decode_kernel_shapes(gpu):
+    # whole-cell staged decode kernel: head groups of 4, 2 and 1, two merge
+    # levels with an explicit mask over two streams, exactly 16 rows per head
+    q, k, v = O.make_inputs(41, B=2, T=1, Hq=32, Hkv=8, n_kv=8192)
+    m = np.full((2, 1, 64, 8192), -np.inf, dtype=np.float16)
+    m[0, 0, 0, :8000] = 0
+    m[1, 0, 0, :6000] = 0
+    m[1, 0, 0, 3000:3100] = -np.inf
+    _check("decode two streams, mask, two-level merge", q, k, v, m, scale=SCALE)
+    q, k, v = O.make_inputs(42, T=1, Hq=24, Hkv=6, n_kv=3000)
+    _check("decode Hkv 6 (head pairs)", q, k, v, scale=SCALE, kv_len=2999)
+    q, k, v = O.make_inputs(43, T=1, Hq=16, Hkv=1, n_kv=5000)
+    _check("decode 16 rows on one kv head", q, k, v, scale=SCALE, kv_len=4990)
+    q, k, v = O.make_inputs(44, T=2, Hq=64, Hkv=8, n_kv=1024)
+    _check("verify T=2 gqa 8:1 (16 rows)", q, k, v, scale=SCALE, kv_len=1000, causal_pos0=998)
