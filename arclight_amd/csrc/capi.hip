@@ -308,8 +308,9 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     // Many query rows with implicit masking: the prefill kernel, one
     // workgroup per 64-row tile, when that alone fills the device.
     const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
+    // (it keeps the running max on scores as computed: needs scale > 0 unless softcapped)
     if (!m.data && p.R > 32 && prefill_tiles * Hkv * B >= n_cu && lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
-        prefer_prefill()) {
+        (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill()) {
         pl.kernel = kPrefill;
         pl.rows_per_tile = kFattnPrefillRows;
         p.n_row_tiles = (int32_t) prefill_tiles;

@@ -369,4 +369,74 @@ __device__ __forceinline__ void process_tile(Tile<RB> & cur, const int cb, const
     apply_tile<RB>(cur, s, full, vis_any, g, o, m_run, l_run);
 }
 
+// ---------------------------------------------------------------------------
+// LDS-DMA staging helpers
+// ---------------------------------------------------------------------------
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef int int4v __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4v;
+
+// s_waitcnt immediates (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8; all-ones = no wait)
+constexpr int vmcnt_imm(int v) { return (v & 15) | ((v >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+__device__ __forceinline__ floatx4 mfma_16x16x16(half4 a, half4 b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane s supplies 8 bytes (4 f16)
+// that form elements 4(s%4)..4(s%4)+3 of row s/4 of a 4 x 16 matrix; lane i
+// receives column i, i.e. element i%4 of the 8 bytes of lanes i/4, 4+i/4,
+// 8+i/4 and 12+i/4.
+__device__ __forceinline__ half4 lds_read_tr16(const char * p) {
+    const short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4v *) p);
+    return __builtin_bit_cast(half4, r);
+}
+
+__device__ __forceinline__ void mem_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::: "memory");
+}
+
+// Raw buffer descriptor (the layout make_rsrc builds) for the inline DMA.
+__device__ __forceinline__ int4v raw_desc(const void * base, uint32_t bytes) {
+    const uint64_t a = (uint64_t) base;
+    return int4v{(int) (uint32_t) a, (int) (uint32_t) (a >> 32), (int) bytes, 0x00020000};
+}
+
+// One LDS-DMA load: 16 bytes per lane from desc + voff into LDS at
+// lds_base + 16 * lane. M0 carries the LDS address; nothing else in these
+// kernels uses M0 (the compiler warns that a clobbered reserved register is
+// not preserved, which is the intent here).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const int4v desc, uint32_t voff, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(desc), "s"(lds_base)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ __forceinline__ uint32_t lds_addr(const void * p) {
+    return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) char *) p;
+}
+
+// Waits until at most `later` stages of PER memory operations each are still
+// outstanding (the stages issued after the one about to be read).
+template <int NB, int PER>
+__device__ __forceinline__ void wait_stage(int later) {
+    mem_barrier();
+    if constexpr (NB >= 4) {
+        if (later >= 2) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); mem_barrier(); return; }
+    }
+    if constexpr (NB >= 3) {
+        if (later >= 1) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); mem_barrier(); return; }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    mem_barrier();
+}
+
 }  // namespace fattn
