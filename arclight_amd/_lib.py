@@ -50,6 +50,25 @@ SIGNATURES = {
     "al_util_fill_randn_f16": (_I, [_VP, _U64, _U64, _U64, _VP]),
     "al_util_f32_to_f16": (_I, [_VP, _VP, _U64, _VP]),
     "al_util_copy_kernel": (_I, [_VP, _VP, _U64, _VP]),
+    # include/arclight_kv.h
+    "al_kv_cells_create": (_I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int32,
+                                ctypes.POINTER(_VP)]),
+    "al_kv_cells_destroy": (_I, [_VP]),
+    "al_kv_cells_clear": (_I, [_VP]),
+    "al_kv_cells_place": (_I, [_VP, ctypes.POINTER(abi.AlUbatch), _VP] + [ctypes.POINTER(ctypes.c_uint32)] * 3),
+    "al_kv_cells_seq_rm": (_I, [_VP, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32]),
+    "al_kv_cells_state": (_I, [_VP, _VP, _VP]),
+    "al_kv_cells_mask_host": (_I, [_VP, ctypes.POINTER(abi.AlUbatch), ctypes.c_uint32, ctypes.c_uint32, _VP]),
+    "al_kv_cells_mask_device": (_I, [_VP, ctypes.POINTER(abi.AlUbatch), ctypes.c_uint32, ctypes.c_uint32,
+                                     ctypes.POINTER(abi.AlTensor), _VP]),
+    "al_kv_cells_implicit": (_I, [_VP, ctypes.POINTER(abi.AlUbatch), ctypes.c_uint32,
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
+    "al_kv_ring_create": (_I, [ctypes.POINTER(abi.AlKvRingParams), ctypes.POINTER(_VP)]),
+    "al_kv_ring_destroy": (_I, [_VP]),
+    "al_kv_ring_cells": (_VP, [_VP]),
+    "al_kv_ring_view_k": (_I, [_VP] + [ctypes.c_uint32] * 4 + [ctypes.POINTER(abi.AlTensor)]),
+    "al_kv_ring_view_v": (_I, [_VP] + [ctypes.c_uint32] * 4 + [ctypes.POINTER(abi.AlTensor)]),
+    "al_kv_ring_write": (_I, [_VP, ctypes.c_uint32] + [ctypes.POINTER(abi.AlTensor)] * 3 + [_VP]),
 }
 
 _lib = None

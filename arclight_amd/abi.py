@@ -103,3 +103,24 @@ def tensor_desc(data, typ, shape, strides, axes):
     ne = [int(shape[a]) for a in axes]
     nb = [int(strides[a]) for a in axes]
     return make_tensor(data, typ, ne, nb)
+
+
+# include/arclight_kv.h
+class AlUbatch(ctypes.Structure):
+    _fields_ = [
+        ("n_tokens", ctypes.c_int32),
+        ("pos", ctypes.POINTER(ctypes.c_int32)),
+        ("seq_mask", ctypes.POINTER(ctypes.c_uint64)),
+    ]
+
+
+class AlKvRingParams(ctypes.Structure):
+    _fields_ = [
+        ("n_layer", ctypes.c_uint32),
+        ("kv_size", ctypes.c_uint32),
+        ("n_seq_max", ctypes.c_uint32),
+        ("n_pad", ctypes.c_uint32),
+        ("n_head_kv", ctypes.c_uint32),
+        ("head_dim", ctypes.c_uint32),
+        ("unified", ctypes.c_int32),
+    ]
