@@ -281,6 +281,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     FattnParams & p = pl.p;
     memset(&p, 0, sizeof(p));
     p.q = (const char *) q.data; p.q_nb1 = q.nb[1]; p.q_nb2 = q.nb[2]; p.q_nb3 = q.nb[3];
+    const uint64_t q_slice = (uint64_t) (T - 1) * q.nb[1] + (uint64_t) (Hq - 1) * q.nb[2] + (uint64_t) D * 4;
+    p.q_bytes = (uint32_t) std::min<uint64_t>(q_slice, INT32_MAX);
     p.k = (const char *) k.data; p.k_nb1 = k.nb[1]; p.k_nb2 = k.nb[2]; p.k_nb3 = k.nb[3];
     p.v = (const char *) v.data; p.v_nb1 = v.nb[1]; p.v_nb2 = v.nb[2]; p.v_nb3 = v.nb[3];
     if (m.data) {
@@ -331,7 +333,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     const bool mask_ok = !m.data || (p.m_slice_bytes < INT32_MAX && aligned16(m.data) && m.nb[1] % 16 == 0 &&
                                      m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
     const int64_t decode_units = Hkv * B;
-    if (p.R <= 16 && prefer_decode() && (size_t) lds_per_block >= decode_lds && mask_ok &&
+    if (p.R <= 16 && prefer_decode() && (size_t) lds_per_block >= decode_lds && mask_ok && q_slice < INT32_MAX &&
         decode_units * sizeof(unsigned) <= kFattnCounterBytes &&
         (uint64_t) (n_kv + 16) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
         (uint64_t) (n_kv + 16) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX) {

@@ -53,6 +53,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     constexpr int REC = 16 * kRowStride;                  // floats of one 16-row state record
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
+    __shared__ __attribute__((aligned(1024))) char qlds[16 * 512];  // the 16 query rows, f32
     __shared__ int s_last;
 
     const int lane = threadIdx.x & 63;
@@ -132,26 +133,40 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         if constexpr (HAS_MASK) dma16(md, msrc + cs * 2, base + 8192u);
     };
 
-    // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
-    // (converted before the first DMA: the compiler does not count the DMA,
-    // so a wait for q after it would wait for every stage in flight)
-    half8 qf[4];
+    // The query rows travel by LDS-DMA too, ahead of the first stages, so
+    // their latency overlaps the K/V loads: DMA block i holds rows 2i (lanes
+    // 0..31) and 2i + 1 (lanes 32..63), 512 bytes each, and is loaded by wave
+    // i % WS. Granule j of row r sits at slot j ^ 2(r & 15), which spreads
+    // the 16 rows' reads below over the LDS banks.
     {
-        const float * qrow = (const float *) (p.q + (int64_t) b * p.q_nb3 + (int64_t) tok * p.q_nb1 +
-                                              (int64_t) head * p.q_nb2);
-        float4 qa[4], qb[4];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            qa[kb] = *(const float4 *) (qrow + 8 * (4 * kb + g));
-            qb[kb] = *(const float4 *) (qrow + 8 * (4 * kb + g) + 4);
+        const int rr = 2 * ws + (lane >> 5);
+        const uint32_t qslot = (uint32_t) (lane & 31);
+        const int4v qd = raw_desc(p.q + (int64_t) b * p.q_nb3, p.q_bytes);
+        for (int i = ws, r2 = rr; i < (rows_here + 1) / 2; i += WS, r2 += 2 * WS) {
+            const int rq = r2 < rows_here ? r2 : 0;
+            const uint32_t qofs = (uint32_t) ((rq / p.G) * p.q_nb1 + (kvh * p.G + rq % p.G) * p.q_nb2);
+            dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r2 & 15))) & 31) * 16, lds_addr(qlds) + (uint32_t) (i * 1024));
         }
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) qf[kb] = rvalid ? to_half8(qa[kb], qb[kb]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    mem_barrier();
 #pragma unroll
     for (int u = 0; u < NB - 1; ++u)
         if (u < my_ns) issue(u, u);
+    // own query rows landed (the stages were issued after them), then everyone's
+    wait_later<NB - 1, PER>(min(NB - 1, my_ns));
+    __syncthreads();
+
+    // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
+    half8 qf[4];
+    {
+        const char * qrow = qlds + n * 512;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const int j = 2 * (4 * kb + g);                               // granules j, j + 1 of row n
+            const float4 qa = *(const float4 *) (qrow + ((j ^ (2 * n)) & 31) * 16);
+            const float4 qb = *(const float4 *) (qrow + (((j + 1) ^ (2 * n)) & 31) * 16);
+            qf[kb] = rvalid ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+    }
 
     float slope = 1.0f;
     if (p.max_bias > 0.0f) {                                           // arm.cpp:2294
@@ -322,49 +337,63 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
 
     // Last workgroup: two adjacent lanes per (row, 4 dims), each taking 16
-    // of the at most 32 splits with all their loads in flight, then
-    // combining with its partner (split half 0 first, on both lanes).
+    // of the at most 32 splits, then combining with its partner (split half
+    // 0 first, on both lanes). A thread takes two such items per round with
+    // all 64 of their loads in flight, so a decode merge (4 rows = 256
+    // items) is one round trip.
     constexpr int kHalf = kMaxSplit / 2;
-    for (int idx = threadIdx.x; idx < rows_here * 64; idx += WS * 64) {
-        const int half = idx & 1;
-        const int d4 = (idx >> 1) & 31;
-        const int rr = idx >> 6;
-        float2 ml[kHalf];
-        float4 ov[kHalf];
+    const int n_items = rows_here * 64;
+    for (int base = 0; base < n_items; base += 2 * WS * 64) {
+        float2 ml[2][kHalf];
+        float4 ov[2][kHalf];
 #pragma unroll
-        for (int j = 0; j < kHalf; ++j) {
-            const int sp = half * kHalf + j;
-            if (sp < p.n_split) {
-                const uint32_t row = (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4);
-                ml[j] = buf_load8_dev(pr, row + 128 * 4);
-                ov[j] = buf_load16_dev(pr, row + d4 * 16);
-            } else {
-                ml[j] = float2{-AL_INF, 0.0f};
-                ov[j] = float4{0, 0, 0, 0};
+        for (int it2 = 0; it2 < 2; ++it2) {
+            const int idx = base + it2 * WS * 64 + threadIdx.x;
+            const int half = idx & 1;
+            const int d4 = (idx >> 1) & 31;
+            const int rr = idx < n_items ? idx >> 6 : 0;
+#pragma unroll
+            for (int j = 0; j < kHalf; ++j) {
+                const int sp = half * kHalf + j;
+                if (sp < p.n_split) {
+                    const uint32_t row = (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4);
+                    ml[it2][j] = buf_load8_dev(pr, row + 128 * 4);
+                    ov[it2][j] = buf_load16_dev(pr, row + d4 * 16);
+                } else {
+                    ml[it2][j] = float2{-AL_INF, 0.0f};
+                    ov[it2][j] = float4{0, 0, 0, 0};
+                }
             }
         }
-        float Mh = ml[0].x;
 #pragma unroll
-        for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[j].x);
-        const float M = fmaxf(Mh, __shfl_xor(Mh, 1));
-        const float Mu = (M == -AL_INF) ? 0.0f : M;
-        float Lh = 0.0f;
-        float4 ah = {0, 0, 0, 0};
+        for (int it2 = 0; it2 < 2; ++it2) {
+            const int idx = base + it2 * WS * 64 + threadIdx.x;
+            const int half = idx & 1;
+            const int d4 = (idx >> 1) & 31;
+            const int rr = idx >> 6;
+            float Mh = ml[it2][0].x;
 #pragma unroll
-        for (int j = 0; j < kHalf; ++j) {
-            const float w = exp_fast(ml[j].x - Mu);
-            Lh += w * ml[j].y;
-            ah.x += w * ov[j].x; ah.y += w * ov[j].y; ah.z += w * ov[j].z; ah.w += w * ov[j].w;
-        }
-        const float Lo = __shfl_xor(Lh, 1);
-        const float4 ao = {__shfl_xor(ah.x, 1), __shfl_xor(ah.y, 1), __shfl_xor(ah.z, 1), __shfl_xor(ah.w, 1)};
-        if (half == 0) {
-            const float L = Lh + Lo;
-            const float4 acc = {ah.x + ao.x, ah.y + ao.y, ah.z + ao.z, ah.w + ao.w};
-            const int t = rr / p.G;
-            const int hq = kvh * p.G + rr % p.G;
-            float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
-            *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
+            for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[it2][j].x);
+            const float M = fmaxf(Mh, __shfl_xor(Mh, 1));
+            const float Mu = (M == -AL_INF) ? 0.0f : M;
+            float Lh = 0.0f;
+            float4 ah = {0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < kHalf; ++j) {
+                const float w = exp_fast(ml[it2][j].x - Mu);
+                Lh += w * ml[it2][j].y;
+                ah.x += w * ov[it2][j].x; ah.y += w * ov[it2][j].y; ah.z += w * ov[it2][j].z; ah.w += w * ov[it2][j].w;
+            }
+            const float Lo = __shfl_xor(Lh, 1);
+            const float4 ao = {__shfl_xor(ah.x, 1), __shfl_xor(ah.y, 1), __shfl_xor(ah.z, 1), __shfl_xor(ah.w, 1)};
+            if (half == 0 && idx < n_items) {
+                const float L = Lh + Lo;
+                const float4 acc = {ah.x + ao.x, ah.y + ao.y, ah.z + ao.z, ah.w + ao.w};
+                const int t = rr / p.G;
+                const int hq = kvh * p.G + rr % p.G;
+                float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
+                *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
+            }
         }
     }
 }

@@ -8,6 +8,7 @@
 // al_fattn_args descriptors. Byte strides; pointers are device pointers.
 struct FattnParams {
     const char * q;     int64_t q_nb1, q_nb2, q_nb3;     // f32 [D, T, Hq, B]
+    uint32_t q_bytes;                                    // bytes of one q stream slice, clamped
     const char * k;     int64_t k_nb1, k_nb2, k_nb3;     // f16 [D, n_kv, Hkv, Bk]
     const char * v;     int64_t v_nb1, v_nb2, v_nb3;     // f16 [D, n_kv, Hkv, Bv]
     const char * mask;  int64_t m_nb1, m_nb2, m_nb3;     // f16 [m_ne0, rows, m_ne2, m_ne3] or null

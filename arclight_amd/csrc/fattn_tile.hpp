@@ -439,4 +439,23 @@ __device__ __forceinline__ void wait_stage(int later) {
     mem_barrier();
 }
 
+// Waits until at most k * PER memory operations are outstanding (0 <= k <=
+// KMAX <= 3): the k stages issued after the data about to be read.
+template <int KMAX, int PER>
+__device__ __forceinline__ void wait_later(int k) {
+    static_assert(KMAX <= 3 && 3 * PER < 64, "vmcnt holds at most 63");
+    mem_barrier();
+    if constexpr (KMAX >= 3) {
+        if (k >= 3) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * PER)); mem_barrier(); return; }
+    }
+    if constexpr (KMAX >= 2) {
+        if (k >= 2) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); mem_barrier(); return; }
+    }
+    if constexpr (KMAX >= 1) {
+        if (k >= 1) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); mem_barrier(); return; }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    mem_barrier();
+}
+
 }  // namespace fattn

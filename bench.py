@@ -12,8 +12,11 @@ is read cold from HBM), replayed as one captured HIP graph.
 Prints one JSON line. `value` is the KV read bandwidth of the whole step:
 algorithmic bytes (K+V of the visible cells, + Q + O) / step time. Extra
 fields report 2048-token chunked causal prefill TFLOP/s (4 chunks of 512 over
-36 layers), the roofline of the decode kernel from per-launch HIP events, and
-the CPU baseline (the f32 restatement of the reference kernel on host cores).
+36 layers), the roofline of the decode kernel from per-launch HIP events,
+the other workloads of the family (decode at 4K / 16K, speculative verify
+with 4 / 8 drafts at 8K, Qwen3-32B-shape decode at 32K and prefill of 4096
+tokens in 1024-token chunks) and the CPU baseline (the f32 restatement of the
+reference kernel on host cores).
 """
 import argparse
 import ctypes
@@ -43,6 +46,8 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the 4K/16K decode, 8K verify and Qwen3-32B-shape lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
     ap.add_argument("--only", choices=["decode", "prefill", "copy"], default=None,
                     help="run one workload only (for profiling); prints its own JSON line")
@@ -119,13 +124,23 @@ def prefill_flops(T_total, chunk, Hq, D):
     return 4 * D * Hq * pairs
 
 
-def bench_decode(lib, stream, a):
-    Hq, Hkv, D, L, ctx = 32, 8, 128, a.layers, a.ctx
+def bench_decode(lib, stream, a, ctx=None, L=None, Hq=32, T=1, steps=None):
+    """Decode (T = 1) or speculative verify (T drafts at positions ctx..ctx+T-1,
+    causal among them) over L layers, each with its own cache slice of
+    PAD(ctx + T, 256) cells."""
+    Hkv, D = 8, 128
+    ctx = ctx or a.ctx
+    L = L or a.layers
     scale = 1.0 / math.sqrt(D)
-    lay = Layers(L, 1, Hq, Hkv, D, ctx, a.seed)
-    args = [lay.args(l, stream, scale, kv_len=ctx) for l in range(L)]
-    ms = time_graph(lib, stream, args, a.steps, a.warmup)
-    byts = decode_bytes(ctx, Hq, Hkv, D)
+    n_kv = (ctx + T + 255) // 256 * 256 if T > 1 else ctx
+    lay = Layers(L, T, Hq, Hkv, D, n_kv, a.seed)
+    if T == 1:
+        args = [lay.args(l, stream, scale, kv_len=ctx) for l in range(L)]
+        byts = decode_bytes(ctx, Hq, Hkv, D)
+    else:
+        args = [lay.args(l, stream, scale, kv_len=ctx + T, causal_pos0=ctx) for l in range(L)]
+        byts = 2 * (ctx + T) * Hkv * D * 2 + 2 * T * Hq * D * 4
+    ms = time_graph(lib, stream, args, steps or a.steps, a.warmup)
     # the timed region is L back-to-back launches of the decode kernel on this
     # stream, so its average launch duration is ms / L
     return {
@@ -136,16 +151,18 @@ def bench_decode(lib, stream, a):
     }
 
 
-def bench_prefill(lib, stream, a):
-    Hq, Hkv, D, L = 32, 8, 128, a.layers
-    T_total, chunk = 2048, 512
+def bench_prefill(lib, stream, a, T_total=2048, chunk=512, Hq=32, L=None):
+    """Causal chunked prefill: chunk c of every layer attends cells
+    [0, chunk (c + 1)), causal within the chunk; chunks run in order, all
+    layers of a chunk before the next chunk, as the model does."""
+    Hkv, D = 8, 128
+    L = L or a.layers
     scale = 1.0 / math.sqrt(D)
     lay = Layers(L, T_total, Hq, Hkv, D, T_total, a.seed + 1)
     from arclight_amd import abi, device
     args = []
     for c in range(T_total // chunk):
         for l in range(L):
-            # chunk c: tokens 512c..512c+511 against cells [0, 512(c+1)), causal within the chunk
             q = lay.q[l]
             qv = device.DeviceTensor(q.buf, abi.AL_TYPE_F32, (1, chunk, Hq, D), None,
                                      c * chunk * Hq * D * 4, abi.Q_AXES)
@@ -156,6 +173,36 @@ def bench_prefill(lib, stream, a):
     fl = prefill_flops(T_total, chunk, Hq, D)
     return {"ms_per_step": ms, "flops_per_layer": fl, "tflops": fl * L / (ms * 1e-3) / 1e12,
             "kernel_ms_mean": ms / len(args)}
+
+
+def bench_other_configs(lib, stream, a):
+    """The remaining workloads of the metric's family, one line each: decode
+    at 4K and 16K, speculative verify at 8K context with 4 and 8 drafts
+    (Qwen3-8B attention shape = Qwen3-4B's), and the Qwen3-32B shape (64
+    query heads, 64 layers) for decode at 32K and 4096-token prefill in
+    1024-token chunks."""
+    out = []
+    steps = max(2, a.steps // 2)
+
+    def dec(name, **kw):
+        r = bench_decode(lib, stream, a, steps=steps, **kw)
+        out.append({"workload": name, "value": round(r["gbs"], 1), "unit": "GB/s",
+                    "hbm_peak_frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                    "us_per_layer": round(r["kernel_ms_mean"] * 1e3, 2)})
+        print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
+
+    dec("decode, Qwen3-4B shape, context 4096, 36 layers", ctx=4096, L=36)
+    dec("decode, Qwen3-4B shape, context 16384, 36 layers", ctx=16384, L=36)
+    dec("verify 4 drafts, Qwen3-8B shape, context 8192, 36 layers", ctx=8192, L=36, T=4)
+    dec("verify 8 drafts, Qwen3-8B shape, context 8192, 36 layers", ctx=8192, L=36, T=8)
+    dec("decode, Qwen3-32B shape (Hq 64), context 32768, 64 layers", ctx=32768, L=64, Hq=64)
+    r = bench_prefill(lib, stream, a, T_total=4096, chunk=1024, Hq=64, L=64)
+    out.append({"workload": "prefill 4096 tokens in 4 causal chunks of 1024, Qwen3-32B shape (Hq 64), 64 layers",
+                "value": round(r["tflops"], 2), "unit": "TFLOP/s",
+                "mfma_peak_frac": round(r["tflops"] / F16_PEAK_TFLOPS, 4),
+                "us_per_launch": round(r["kernel_ms_mean"] * 1e3, 2)})
+    print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
+    return out
 
 
 def bench_copy(stream, nbytes=1 << 30):
@@ -221,7 +268,8 @@ def main():
     a = parse()
     if a.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                          "(attention would shard by KV head across GPUs, see DESIGN.md)"}))
+                          "(attention would shard by KV head across GPUs, with no exchange before "
+                          "the output projection)"}))
         sys.exit(2)
     from arclight_amd import _lib, device
     lib = _lib.load()
@@ -244,6 +292,7 @@ def main():
     pre = None if a.no_prefill else bench_prefill(lib, stream, a)
     if pre:
         print(f"[bench] prefill {pre}", file=sys.stderr, flush=True)
+    others = None if a.no_other_configs else bench_other_configs(lib, stream, a)
     cpu = None if a.no_cpu_baseline else cpu_baseline(a)
     if cpu:
         print(f"[bench] cpu {cpu}", file=sys.stderr, flush=True)
@@ -278,6 +327,7 @@ def main():
             "tflops": round(pre["tflops"], 2),
             "mfma_peak_frac": round(pre["tflops"] / F16_PEAK_TFLOPS, 4),
             "ms_per_step": round(pre["ms_per_step"], 4)},
+        "other_configs": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out))
