@@ -312,6 +312,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
     // (it keeps the running max on scores as computed: needs scale > 0 unless softcapped)
     if (!m.data && p.R > 32 && prefill_tiles * Hkv * B >= n_cu && lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
+        q_slice < INT32_MAX &&
         (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill()) {
         pl.kernel = kPrefill;
         pl.rows_per_tile = kFattnPrefillRows;
@@ -424,6 +425,8 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
         pl.p.counters = (unsigned *) ws;
         pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
     }
+    rc = al_device_error_flag(&pl.p.err);
+    if (rc != AL_OK) return rc;
     hipError_t e;
     switch (pl.kernel) {
         case kPrefill: e = fattn_prefill_launch(pl.p, (hipStream_t) a->stream); break;
@@ -442,13 +445,14 @@ extern "C" int al_device_errors(void) {
     int * flag = nullptr;
     int rc = al_device_error_flag(&flag);
     if (rc != AL_OK) return rc;
-    int h[2] = {0, 0};
+    int h[4] = {0, 0, 0, 0};
     hipError_t e = hipMemcpy(h, flag, sizeof(h), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return al_hip_fail(e, "hipMemcpy(error flag)");
-    if (h[0]) {
+    if (h[0] || h[2]) {
         e = hipMemset(flag, 0, sizeof(h));
         if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
-        return al_fail(AL_ERR_INVALID, "set_rows: row index %d out of range (ops.cpp:171)", h[1]);
+        if (h[0]) return al_fail(AL_ERR_INVALID, "set_rows: row index %d out of range (ops.cpp:171)", h[1]);
+        return al_fail(AL_ERR_HIP, "fattn prefill: a wave gave up waiting for its partner's tile hand-off");
     }
     return AL_OK;
 }

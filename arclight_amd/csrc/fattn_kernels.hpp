@@ -33,6 +33,7 @@ struct FattnParams {
     int32_t interleave;             // decode kernel: splits take every n_split-th 16-cell stage
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
+    int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).

@@ -5,16 +5,18 @@
 //
 // One workgroup = one row tile of 64 query rows of one kv-head group
 // (row r -> token r / G, head kvh*G + r % G) and 8 wavefronts, two per SIMD.
-// Wave w holds row half w & 1 (32 rows: 2 MFMA row blocks, so each K/V
+// Wave w takes row half w & 1 (32 rows: 2 MFMA row blocks, so each K/V
 // operand read from LDS feeds 2 MFMAs) and cell split w >> 1 (every 4th
-// 32-cell tile of the visible range). The two waves of a split share its
-// LDS stages, one loading K and the other V, and every wave passes two
-// workgroup barriers per tile (tile landed; tile read). The 4 splits'
-// online-softmax states merge through LDS at the end. A 512-token chunk of
-// Qwen3-4B gives 32 row tiles x 8 kv heads = 256 workgroups.
+// 32-cell tile of the visible range). The two waves of a split sit on
+// different SIMDs and share the split's ring of two 16 KiB LDS stages: the
+// row-half-0 wave loads the tiles, publishes "tile landed" in an LDS flag,
+// and refills a stage once the row-half-1 wave has published "tile read".
+// No workgroup barrier runs in the loop, so the splits drift apart and the
+// two waves on each SIMD (different splits) overlap each other's matrix and
+// vector work. A 512-token chunk of Qwen3-4B gives 32 row tiles x 8 kv heads
+// = 256 workgroups, one per CU.
 //
-// K/V tiles travel HBM/L2 -> LDS by LDS-DMA buffer loads, two 16 KiB stages
-// per split in flight without costing registers:
+// K/V tiles travel HBM/L2 -> LDS by LDS-DMA buffer loads:
 //   - K as MFMA A operands: block (mb, kb) holds, at lane l's 16-byte slot,
 //     cell 16 mb + l % 16, dims 32 kb + 8 (l / 16) .. + 7, so ds_read_b128
 //     at lane*16 yields the operand;
@@ -22,8 +24,10 @@
 //     at slot j ^ (c & 15), read transposed by ds_read_b64_tr_b16 into V^T
 //     A operands whose k slots follow the S^T output layout (cells 4g + i
 //     and 16 + 4g + i of lane group g), so P^T is S^T in place.
-// The DMA is inline assembly the compiler does not count; each wave waits
-// for its own loads (s_waitcnt vmcnt), the barrier for its partner's.
+// The DMA is inline assembly the compiler does not count; the loading wave
+// waits for its tile (s_waitcnt vmcnt) before publishing it. The query rows
+// come the same way, once per workgroup, into a staging area that holds the
+// flags afterwards.
 //
 // Softmax per tile: the running max is kept on the raw scores (scale > 0
 // keeps their order), p = exp2(s * c - m * c) with c = scale * log2(e) is
@@ -31,7 +35,8 @@
 // and the row sums l come from an extra MFMA against an all-ones operand
 // (f32 accumulation of the same f16 P that weights V). The reference max
 // moves lazily (only when a tile exceeds it by more than kTau in natural
-// units), so O is rarely rescaled.
+// units), so O is rarely rescaled; the rescale runs outside the fast loop so
+// the accumulators stay in place across iterations.
 //
 // The 1-D grid runs kv head fastest (XCD affinity: with Hkv = 8 each head's
 // K/V stays in one XCD's L2) and, with a causal mask, row tiles longest
@@ -50,15 +55,86 @@ constexpr int kPRB = 2;                      // MFMA row blocks per wave
 constexpr int kPRows = 16 * kPRB * kRH;      // query rows per workgroup
 constexpr int kKBytes = 8 * 1024;            // K of a 32-cell tile: 8 MFMA-ordered 1 KiB blocks
 constexpr int kStage = 2 * kKBytes;          // K then V (32 cells x 256 bytes)
+constexpr int kNB = 2;                       // stages per split
+constexpr int kStride = kCS * 32;            // cells between a split's tiles
+constexpr int kRing = kCS * kNB * kStage;    // 128 KiB
+constexpr int kQBytes = kPRows * 512;        // the tile's query rows, f32 (32 KiB)
+constexpr int kRec = kPRows * kRowStride * 4;        // one split's merge record (64 rows)
+constexpr int kLds = kCS * kRec > kRing + kQBytes ? kCS * kRec : kRing + kQBytes;   // 160 KiB
 constexpr float kLog2e = 1.44269504088896341f;
+constexpr int kSpinLimit = 1 << 22;          // flag polls before a wave gives up (never in a correct run)
 
-struct PTile {
-    u32x4 k[2][4];                           // [mb][kb] K A-operand chunks
-    half8 vt[8];                             // V^T A operands, dim block d: rows 16d..16d+15
+// The operands of one tile in registers.
+struct TileOps {
+    u32x4 k[2][4];                           // K A operands [mb][kb]
+    half8 vt[8];                             // V^T A operands, dim block d
 };
 
+// LDS-DMA of tile (cells cb ..) into a stage: 8 K blocks, then 8 V blocks.
+__device__ __forceinline__ void issue_tile(const int4v kd, const int4v vd, const uint32_t base, const uint32_t cb,
+                                           const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n) {
+    const uint32_t kofs = (cb + (uint32_t) n) * k_nb1 + (uint32_t) (g * 16);
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            dma16(kd, kofs + (uint32_t) (16 * mb) * k_nb1 + (uint32_t) (64 * kb), base + (uint32_t) ((mb * 4 + kb) * 1024));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = 4 * i + g;
+        dma16(vd, (cb + (uint32_t) c) * v_nb1 + (uint32_t) (((n ^ c) & 15) * 16), base + (uint32_t) (kKBytes + i * 1024));
+    }
+}
+
+// Both operands of a stage: K at lane*16 of each block; V^T from source
+// cells 4g + (n >> 2) (k slots 0..3) and 16 + 4g + (n >> 2) (4..7), dims
+// 16d + 4(n & 3) .. + 3 (granule 2d + ((n & 3) >> 1), half n & 1).
+__device__ __forceinline__ void read_tile(TileOps & t, const char * st, const int lane, const int g, const int n) {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) t.k[mb][kb] = *(const u32x4 *) (st + (mb * 4 + kb) * 1024 + lane * 16);
+    const int vc0 = 4 * g + (n >> 2);
+    const int vc1 = 16 + vc0;
+    const int vq = (n & 3) >> 1;
+    const char * r0 = st + kKBytes + vc0 * 256 + (n & 1) * 8;
+    const char * r1 = st + kKBytes + vc1 * 256 + (n & 1) * 8;
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        const half4 a = lds_read_tr16(r0 + (((2 * d + vq) ^ (vc0 & 15)) << 4));
+        const half4 c = lds_read_tr16(r1 + (((2 * d + vq) ^ (vc1 & 15)) << 4));
+        t.vt[d] = half8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+    }
+}
+
+// LDS flag hand-off between the two waves of a split.
+__device__ __forceinline__ void flag_set(int * f, int v) {
+    __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Waits until *f >= v; false if it never got there (a broken hand-off),
+// so the wave ends instead of hanging.
+__device__ __forceinline__ bool flag_wait(const int * f, int v) {
+    for (int i = 0; i < kSpinLimit; ++i) {
+        if (__hip_atomic_load(const_cast<int *>(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return true;
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return false;
+}
+
+// After the softmax of tile it, the loading wave refills the tile's stage
+// with tile it + 2 once the other wave has read it.
+__device__ __forceinline__ bool refill(const bool loader, const int it, const int nt, const int * done, const int4v kd,
+                                       const int4v vd, const uint32_t ring_addr, const int cb0, const uint32_t k_nb1,
+                                       const uint32_t v_nb1, const int g, const int n) {
+    if (!loader || it + 2 >= nt) return true;
+    const bool ok = flag_wait(done, it);
+    if (ok) issue_tile(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) (cb0 + (it + 2) * kStride), k_nb1,
+                       v_nb1, g, n);
+    return ok;
+}
+
 // P = exp2(s c - m c) in f16, then O^T += V^T P^T and l += 1 P^T.
-__device__ __forceinline__ void accumulate_tile(PTile & t, const floatx4 (&s)[kPRB][2], const bool full,
+__device__ __forceinline__ void accumulate_tile(TileOps & t, const floatx4 (&s)[kPRB][2], const bool full,
                                                 const bool (&vis_any)[8], const float (&m_run)[kPRB], const float cexp,
                                                 const half8 ones, const int g, floatx4 (&o)[kPRB][8],
                                                 floatx4 (&lacc)[kPRB]) {
@@ -91,7 +167,7 @@ __device__ __forceinline__ void accumulate_tile(PTile & t, const floatx4 (&s)[kP
 
 template <bool SOFTCAP>
 __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnParams p) {
-    __shared__ __attribute__((aligned(1024))) char lds[kCS][2][kStage];
+    __shared__ __attribute__((aligned(1024))) char lds[kLds];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -117,68 +193,62 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int4v kd = raw_desc(kbase, (uint32_t) (p.n_kv - 1) * k_nb1 + 256);
     const int4v vd = raw_desc(vbase, (uint32_t) (p.n_kv - 1) * v_nb1 + 256);
 
-    // this split's tiles: cells cb0 + it * 128; every wave runs the loop
-    // ntiles_max times (the workgroup barriers must match), doing work only
-    // while it < ntiles
-    constexpr int kStride = kCS * 32;
+    // this split's tiles: cells cb0 + it * kStride, it < nt
     const int cb0 = cs * 32;
-    const int ntiles = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
-    const int ntiles_max = hi > 0 ? (hi + kStride - 1) / kStride : 0;
+    const int nt = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
+    const char * ring = &lds[cs * kNB * kStage];
+    const uint32_t ring_addr = lds_addr(ring);
+    const bool loader = rh == 0;
 
-    // DMA of a tile: the row-half-0 wave of the split loads the 8 K blocks
-    // (block (mb, kb) lane (g, n): cell 16 mb + n, granule 4 kb + g), the
-    // row-half-1 wave the 8 V blocks (block i lane (g, n): cell c = 4i + g,
-    // granule n ^ (c & 15) into slot n)
-    const uint32_t ring = lds_addr(&lds[cs][0][0]);
-    const uint32_t ksrc = (uint32_t) n * k_nb1 + (uint32_t) (g * 16);
-    auto issue = [&](const int it, const int u) {
-        const uint32_t cb = (uint32_t) (cb0 + it * kStride);
-        const uint32_t base = ring + (uint32_t) (u * kStage);
-        if (rh == 0) {
-            const uint32_t kofs = cb * k_nb1 + ksrc;
+    // The tile's query rows travel once, by LDS-DMA into the staging area
+    // behind the rings, ahead of the first K/V tiles: wave w loads rows
+    // 8w .. 8w + 7 (block i = rows 2i, 2i + 1 of 512 bytes each). Granule j
+    // of row r sits at slot j ^ 2(r & 15), which spreads the reads below over
+    // the LDS banks.
+    char * qst = &lds[kRing];
+    {
+        const int4v qd = raw_desc(p.q + (int64_t) b * p.q_nb3, p.q_bytes);
+        const uint32_t qslot = (uint32_t) (lane & 31);
 #pragma unroll
-            for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                for (int kb = 0; kb < 4; ++kb)
-                    dma16(kd, kofs + (uint32_t) (16 * mb) * k_nb1 + (uint32_t) (64 * kb), base + (uint32_t) ((mb * 4 + kb) * 1024));
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = 4 * i + g;
-                dma16(vd, (cb + (uint32_t) c) * v_nb1 + (uint32_t) (((n ^ c) & 15) * 16), base + (uint32_t) (kKBytes + i * 1024));
-            }
+        for (int i = 0; i < 4; ++i) {
+            const int r = 8 * wave + 2 * i + (lane >> 5);
+            const int rq = r < rows_here ? r : 0;
+            const uint32_t qofs = (uint32_t) (((row0 + rq) / p.G) * p.q_nb1 + (kvh * p.G + (row0 + rq) % p.G) * p.q_nb2);
+            dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r & 15))) & 31) * 16,
+                  lds_addr(qst) + (uint32_t) ((8 * wave + 2 * i) * 512));
         }
-    };
+    }
+    if (loader && nt > 0) issue_tile(kd, vd, ring_addr, (uint32_t) cb0, k_nb1, v_nb1, g, n);
+    if (loader && nt > 1) issue_tile(kd, vd, ring_addr + kStage, (uint32_t) (cb0 + kStride), k_nb1, v_nb1, g, n);
+    wait_later<2, 16>(loader ? min(nt, 2) : 0);                      // own query rows landed
+    __syncthreads();                                                   // everyone's
 
     // query rows held by this lane (column n of its two row blocks) and their
     // Q^T B-operand fragments (k slots of block kb, group g = dims 32kb + 8g..+8)
     int tok[kPRB];
-    int head[kPRB];
     bool rvalid[kPRB];
-    float4 qa[kPRB][4], qb[kPRB][4];
+    half8 qf[kPRB][4];
 #pragma unroll
     for (int rb = 0; rb < kPRB; ++rb) {
         const int rr = 32 * rh + 16 * rb + n;
         rvalid[rb] = rr < rows_here;
         tok[rb] = rvalid[rb] ? (row0 + rr) / p.G : 0;
-        head[rb] = kvh * p.G + (rvalid[rb] ? (row0 + rr) % p.G : 0);
-        const float * qrow = (const float *) (p.q + (int64_t) b * p.q_nb3 + (int64_t) tok[rb] * p.q_nb1 +
-                                              (int64_t) head[rb] * p.q_nb2);
+        const char * qrow = qst + rr * 512;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            qa[rb][kb] = *(const float4 *) (qrow + 8 * (4 * kb + g));
-            qb[rb][kb] = *(const float4 *) (qrow + 8 * (4 * kb + g) + 4);
+            const int j = 2 * (4 * kb + g);                               // granules j, j + 1 of row rr
+            const float4 qa = *(const float4 *) (qrow + ((j ^ (2 * n)) & 31) * 16);
+            const float4 qb = *(const float4 *) (qrow + (((j + 1) ^ (2 * n)) & 31) * 16);
+            qf[rb][kb] = rvalid[rb] ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
-    // the first two tiles fly together with q (converting q waits for all of it)
-    mem_barrier();
-    if (ntiles > 0) issue(0, 0);
-    if (ntiles > 1) issue(1, 1);
-    half8 qf[kPRB][4];
-#pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb)
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) qf[rb][kb] = rvalid[rb] ? to_half8(qa[rb][kb], qb[rb][kb]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+    // the staging area becomes the flags: landed[cs], then done[cs]
+    int * flags = (int *) qst;
+    __syncthreads();
+    if (threadIdx.x < 2 * kCS) flags[threadIdx.x] = -1;
+    __syncthreads();
+    int * landed = flags + cs;
+    const int * done = flags + kCS + cs;
 
     int lim[kPRB];
 #pragma unroll
@@ -204,56 +274,34 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
         for (int d = 0; d < 8; ++d) o[rb][d] = floatx4{0, 0, 0, 0};
     }
 
-    // LDS read offsets of this lane: K at lane*16 of each block; V^T source
-    // cells 4g + (n >> 2) (k slots 0..3) and 16 + 4g + (n >> 2) (4..7),
-    // dims 16d + 4(n & 3) .. + 3 (granule 2d + ((n & 3) >> 1), half n & 1)
-    const int vc0 = 4 * g + (n >> 2);
-    const int vc1 = 16 + vc0;
-    const int vr0 = kKBytes + vc0 * 256 + (n & 1) * 8;
-    const int vr1 = kKBytes + vc1 * 256 + (n & 1) * 8;
-    const int vq = (n & 3) >> 1;
-
     // Tile state shared by the fast loop and the rescale path below.
-    PTile t;
+    TileOps t;
     floatx4 s[kPRB][2];
     float mt[kPRB];
     bool full = true;
     bool vis_any[8];
+    bool ok = true;
 
     // The fast loop never scales O: a tile whose max would move the
     // reference (the first tile always does) leaves it, and the scaling
     // happens outside, so the accumulators stay in MFMA registers across
-    // iterations instead of being copied for a rarely taken branch. Each
-    // tile costs every wave exactly two workgroup barriers, on either path.
+    // iterations instead of being copied for a rarely taken branch.
     int it = 0;
-    while (it < ntiles_max) {
-        for (; it < ntiles_max; ++it) {
-            const bool active = it < ntiles;
-            const int u = it & 1;
-            // this wave's 8 loads of the tile are done once at most the next
-            // tile's 8 are outstanding; the barrier makes the partner's visible
-            if (active) wait_stage<3, 8>(min(1, ntiles - 1 - it));
-            __syncthreads();
-            if (active) {
-                const char * st = &lds[cs][u][0];
-#pragma unroll
-                for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) t.k[mb][kb] = *(const u32x4 *) (st + (mb * 4 + kb) * 1024 + lane * 16);
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    const half4 a = lds_read_tr16(st + vr0 + (((2 * d + vq) ^ (vc0 & 15)) << 4));
-                    const half4 c = lds_read_tr16(st + vr1 + (((2 * d + vq) ^ (vc1 & 15)) << 4));
-                    t.vt[d] = half8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
-                }
-                mem_barrier();
-                __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));             // lgkmcnt(0)
-                mem_barrier();
+    while (it < nt && ok) {
+        for (; it < nt; ++it) {
+            // tile it in its stage: landed (own loads, or the loader's flag)
+            if (loader) {
+                wait_later<1, 16>(it + 1 < nt ? 1 : 0);
+                flag_set(landed, it);
+            } else if (!flag_wait(landed, it)) {
+                ok = false;
+                break;
             }
-            // both waves of the split have read the stage: refill it
-            __syncthreads();
-            if (!active) continue;
-            if (it + 2 < ntiles) issue(it + 2, u);
+            read_tile(t, ring + (it & 1) * kStage, lane, g, n);
+            mem_barrier();
+            __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));                 // lgkmcnt(0): the stage is read
+            mem_barrier();
+            if (!loader) flag_set(landed + kCS, it);                       // done[cs]
             const int cb = cb0 + it * kStride;
 
             // S^T = K Q^T: cells 4g+i (mb 0) and 16+4g+i (mb 1) of row n
@@ -298,8 +346,12 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             }
             if (__any(grow_any)) break;
             accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
+            if (!refill(loader, it, nt, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
+                ok = false;
+                break;
+            }
         }
-        if (it >= ntiles_max) break;
+        if (it >= nt || !ok) break;
         // tile `it` moves the reference max of some rows: scale, then finish it
 #pragma unroll
         for (int rb = 0; rb < kPRB; ++rb) {
@@ -312,8 +364,11 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             m_run[rb] = mn;
         }
         accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
+        ok = refill(loader, it, nt, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
         ++it;
     }
+    if (!ok && lane == 0) atomicOr(p.err + 2, 1);                      // reported by al_device_errors
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                          // no DMA may still target LDS
 
     // natural-unit max and the row sums (every element of lacc holds l)
     float m_nat[kPRB], l_run[kPRB];
@@ -323,61 +378,54 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
         l_run[rb] = lacc[rb][0];
     }
 
-    // merge the kCS splits of each row half through LDS records
-    // [rh][slot][32 rows][132] in two rounds (the stages are free now)
-    float * recs = (float *) &lds[0][0][0];
+    // Merge: every wave publishes its 32-row state to LDS [split][row][132]
+    // (the rings are free once all waves are past their loops), then the
+    // workgroup combines the 4 splits of each (row, 4 dims) and writes it.
+    __syncthreads();
+    float * recs = (float *) &lds[0];
+    {
+        float * rec = recs + cs * (kPRows * kRowStride);
 #pragma unroll
-    for (int span = kCS / 2; span >= 1; span /= 2) {
-        __syncthreads();
-        if (cs >= span && cs < 2 * span) {
-            float * rec = recs + (rh * (kCS / 2) + (cs - span)) * (32 * kRowStride);
+        for (int rb = 0; rb < kPRB; ++rb) {
+            float * row = rec + (32 * rh + 16 * rb + n) * kRowStride;
 #pragma unroll
-            for (int rb = 0; rb < kPRB; ++rb) {
-                float * row = rec + (16 * rb + n) * kRowStride;
-#pragma unroll
-                for (int d = 0; d < 8; ++d) *(float4 *) (row + 16 * d + 4 * g) = float4{o[rb][d][0], o[rb][d][1], o[rb][d][2], o[rb][d][3]};
-                if (g == 0) *(float2 *) (row + 128) = float2{m_nat[rb], l_run[rb]};
-            }
-        }
-        __syncthreads();
-        if (cs < span) {
-            const float * rec = recs + (rh * (kCS / 2) + cs) * (32 * kRowStride);
-#pragma unroll
-            for (int rb = 0; rb < kPRB; ++rb) {
-                const float * row = rec + (16 * rb + n) * kRowStride;
-                const float2 ml = *(const float2 *) (row + 128);
-                const float mn = fmaxf(m_nat[rb], ml.x);
-                const float mu = (mn == -AL_INF) ? 0.0f : mn;
-                const float wa = exp_fast(m_nat[rb] - mu);
-                const float wb = exp_fast(ml.x - mu);
-#pragma unroll
-                for (int d = 0; d < 8; ++d) {
-                    const float4 x = *(const float4 *) (row + 16 * d + 4 * g);
-                    o[rb][d][0] = o[rb][d][0] * wa + x.x * wb;
-                    o[rb][d][1] = o[rb][d][1] * wa + x.y * wb;
-                    o[rb][d][2] = o[rb][d][2] * wa + x.z * wb;
-                    o[rb][d][3] = o[rb][d][3] * wa + x.w * wb;
-                }
-                l_run[rb] = l_run[rb] * wa + ml.y * wb;
-                m_nat[rb] = mn;
-            }
+            for (int d = 0; d < 8; ++d) *(float4 *) (row + 16 * d + 4 * g) = float4{o[rb][d][0], o[rb][d][1], o[rb][d][2], o[rb][d][3]};
+            if (g == 0) *(float2 *) (row + 128) = float2{m_nat[rb], l_run[rb]};
         }
     }
-    if (cs != 0) return;
+    __syncthreads();
 #pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-        if (!rvalid[rb]) continue;
-        float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok[rb]) * p.Hq + head[rb]) * p.dst_nb1);
+    for (int k = 0; k < kPRows * 32 / (kPW * 64); ++k) {
+        const int item = k * kPW * 64 + threadIdx.x;
+        const int rr = item >> 5, d4 = item & 31;
+        if (rr >= rows_here) continue;
+        float2 ml[kCS];
+        float M = -AL_INF;
 #pragma unroll
-        for (int d = 0; d < 8; ++d)
-            *(float4 *) (out + 16 * d + 4 * g) =
-                finalize4(float4{o[rb][d][0], o[rb][d][1], o[rb][d][2], o[rb][d][3]}, m_nat[rb], l_run[rb], p.sinks, head[rb]);
+        for (int c = 0; c < kCS; ++c) {
+            ml[c] = *(const float2 *) (recs + (c * kPRows + rr) * kRowStride + 128);
+            M = fmaxf(M, ml[c].x);
+        }
+        const float Mu = (M == -AL_INF) ? 0.0f : M;
+        float L = 0.0f;
+        float4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < kCS; ++c) {
+            const float w = exp_fast(ml[c].x - Mu);
+            L += w * ml[c].y;
+            const float4 x = *(const float4 *) (recs + (c * kPRows + rr) * kRowStride + 4 * d4);
+            acc.x += w * x.x; acc.y += w * x.y; acc.z += w * x.z; acc.w += w * x.w;
+        }
+        const int tk = (row0 + rr) / p.G;
+        const int hq = kvh * p.G + (row0 + rr) % p.G;
+        float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
+        *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
     }
 }
 
 }  // namespace
 
-size_t fattn_prefill_lds_bytes() { return sizeof(char) * kCS * 2 * kStage; }
+size_t fattn_prefill_lds_bytes() { return (size_t) kLds; }
 
 hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream) {
     const dim3 grid((unsigned) ((int64_t) p.Hkv * p.n_row_tiles * p.B));

@@ -147,8 +147,10 @@ int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
 
 /*
  * Reports and clears errors that kernels recorded on the current device
- * (out-of-range set_rows indices). Call after synchronizing the stream.
- * Returns AL_OK or AL_ERR_INVALID with al_last_error() set.
+ * (out-of-range set_rows indices: AL_ERR_INVALID; a prefill wave that gave
+ * up waiting for its partner wave's tile hand-off, which a correct run
+ * never does: AL_ERR_HIP). Call after synchronizing the stream. Returns
+ * AL_OK or the error with al_last_error() set.
  */
 int al_device_errors(void);
 

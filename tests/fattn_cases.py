@@ -36,4 +36,5 @@ def run_gpu(q, k, v, mask=None, sinks=None, *, scale, max_bias=0.0, logit_softca
     dst = fattn.flash_attn_ext(dq, dk, dv, dm, ds, scale=scale, max_bias=max_bias, logit_softcap=logit_softcap,
                                kv_len=kv_len, causal_pos0=causal_pos0, prec=prec, workspace=workspace)
     device.synchronize()
+    fattn.device_errors()                  # no kernel recorded an error (raises if one did)
     return dst.numpy(np.float32)
