@@ -69,6 +69,9 @@ SIGNATURES = {
     "al_kv_ring_view_k": (_I, [_VP] + [ctypes.c_uint32] * 4 + [ctypes.POINTER(abi.AlTensor)]),
     "al_kv_ring_view_v": (_I, [_VP] + [ctypes.c_uint32] * 4 + [ctypes.POINTER(abi.AlTensor)]),
     "al_kv_ring_write": (_I, [_VP, ctypes.c_uint32] + [ctypes.POINTER(abi.AlTensor)] * 3 + [_VP]),
+    # include/arclight_prologue.h
+    "al_rms_norm_rope_f32": (_I, [ctypes.POINTER(abi.AlTensor)] * 3 + [ctypes.c_float, ctypes.POINTER(abi.AlRopeParams)]
+                             + [ctypes.POINTER(abi.AlTensor)] * 2 + [_VP]),
 }
 
 _lib = None

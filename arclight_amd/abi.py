@@ -124,3 +124,27 @@ class AlKvRingParams(ctypes.Structure):
         ("head_dim", ctypes.c_uint32),
         ("unified", ctypes.c_int32),
     ]
+
+
+# include/arclight_prologue.h
+AL_ROPE_NORMAL = 0
+AL_ROPE_NEOX = 2
+
+
+class AlRopeParams(ctypes.Structure):
+    _fields_ = [
+        ("n_dims", ctypes.c_int32),
+        ("mode", ctypes.c_int32),
+        ("n_ctx_orig", ctypes.c_int32),
+        ("freq_base", ctypes.c_float),
+        ("freq_scale", ctypes.c_float),
+        ("ext_factor", ctypes.c_float),
+        ("attn_factor", ctypes.c_float),
+        ("beta_fast", ctypes.c_float),
+        ("beta_slow", ctypes.c_float),
+    ]
+
+
+def qwen3_rope(n_ctx_orig=40960):
+    """Qwen3's rope_ext parameters (models/qwen3.cpp:49-55)."""
+    return AlRopeParams(128, AL_ROPE_NEOX, n_ctx_orig, 1000000.0, 1.0, 0.0, 1.0, 32.0, 1.0)

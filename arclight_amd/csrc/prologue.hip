@@ -1,0 +1,200 @@
+// Producers of the attention operands for gfx950 (include/arclight_prologue.h):
+// per-head RMSNorm, the norm weight and the rotary embedding of Q and K in
+// one pass, K optionally straight into the f16 KV cache.
+//
+// Semantics: nnml_compute_forward_rms_norm_f32 (nnml/src/ops/ops.cpp:
+// 680-726: squares summed in double, mean and scale in float), the f32 mul,
+// and nnml_compute_forward_rope_f32 (ops.cpp:871-962) with rope_yarn and the
+// rotation cache (ops.cpp:743-772): the angle of pair i is the position
+// multiplied i times by theta_scale in float, exactly as the cache loop
+// carries it.
+//
+// One wavefront per (token, head) row of 128 floats: lane l holds the two
+// elements of rotation pair l (dims l and l + 64 for NEOX, 2l and 2l + 1
+// otherwise), so the norm is one wave reduction and the rotation needs no
+// data exchange. A workgroup takes 4 heads of one token; the pair angles and
+// their cos / sin are computed once per wave.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstring>
+
+#include "../../include/arclight_prologue.h"
+#include "runtime.hpp"
+
+namespace {
+
+struct NormRopeParams {
+    const char * x;     int64_t x_nb1, x_nb2;      // row (head h, token t) at x + h nb1 + t nb2
+    const float * w;                               // [128] or null
+    const int32_t * pos;                           // [T]
+    char * y;           int64_t y_nb1, y_nb2;      // f32 rows, or the f16 cache (nb1 = row bytes)
+    const char * rows;  int64_t rows_nb0;          // cache rows [T] or null
+    int32_t rows64;
+    int64_t n_rows_dst;
+    int32_t H, T;
+    float eps;
+    float theta_scale, freq_scale, ext_factor, corr0, corr1, mscale;
+    int * err;                                     // [2]: first out-of-range cache row
+};
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// MODE: 0 no rotation, 1 pairs (2i, 2i + 1), 2 NEOX pairs (i, i + 64).
+template <int MODE, bool CACHE>
+__global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) {
+    // every product and sum rounded on its own, as the reference's C source
+    // reads: at angles of thousands of radians one ulp of theta moves the
+    // output by ~1e-4, so a fused multiply-add there would not match
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
+    const int t = blockIdx.x;
+    if (h >= p.H) return;
+
+    const int d0 = MODE == 1 ? 2 * lane : lane;
+    const int d1 = MODE == 1 ? 2 * lane + 1 : lane + 64;
+
+    // cos / sin of pair `lane` at this token's position (ops.cpp:743-772)
+    float c = 1.0f, s = 0.0f;
+    if constexpr (MODE != 0) {
+        const float theta_extrap0 = (float) p.pos[t];
+        float theta_extrap = theta_extrap0;
+        for (int k = 0; k < 63; ++k)
+            if (k < lane) theta_extrap *= p.theta_scale;
+        const float theta_interp = p.freq_scale * theta_extrap;
+        float theta = theta_interp;
+        if (p.ext_factor != 0.0f) {
+            const float yv = ((float) lane - p.corr0) / fmaxf(0.001f, p.corr1 - p.corr0);
+            const float ramp = 1.0f - fminf(1.0f, fmaxf(0.0f, yv));
+            const float mix = ramp * p.ext_factor;
+            theta = theta_interp * (1.0f - mix) + theta_extrap * mix;
+        }
+        c = cosf(theta) * p.mscale;
+        s = sinf(theta) * p.mscale;
+    }
+    const float w0 = p.w ? p.w[d0] : 1.0f;
+    const float w1 = p.w ? p.w[d1] : 1.0f;
+
+    const float * xr = (const float *) (p.x + (int64_t) h * p.x_nb1 + (int64_t) t * p.x_nb2);
+    const float x0 = xr[d0];
+    const float x1 = xr[d1];
+    const float sq0 = x0 * x0, sq1 = x1 * x1;
+    const double sum = wave_sum((double) sq0 + (double) sq1);
+    const float mean = (float) (sum / 128.0);
+    const float scale = 1.0f / sqrtf(mean + p.eps);
+    float n0 = x0 * scale, n1 = x1 * scale;
+    if (p.w) {
+        n0 = n0 * w0;
+        n1 = n1 * w1;
+    }
+    float y0 = n0, y1 = n1;
+    if constexpr (MODE != 0) {
+        y0 = n0 * c - n1 * s;
+        y1 = n0 * s + n1 * c;
+    }
+    if constexpr (CACHE) {
+        const char * ip = p.rows + (int64_t) t * p.rows_nb0;
+        const int64_t r = p.rows64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+        if (r < 0 || r >= p.n_rows_dst) {
+            if (lane == 0 && atomicCAS(p.err, 0, 1) == 0) p.err[1] = (int) r;
+            return;
+        }
+        _Float16 * yr = (_Float16 *) (p.y + r * p.y_nb1) + (int64_t) h * 128;
+        yr[d0] = (_Float16) y0;
+        yr[d1] = (_Float16) y1;
+    } else {
+        float * yr = (float *) (p.y + (int64_t) h * p.y_nb1 + (int64_t) t * p.y_nb2);
+        yr[d0] = y0;
+        yr[d1] = y1;
+    }
+}
+
+template <int MODE>
+hipError_t launch_mode(const NormRopeParams & p, bool cache, hipStream_t stream) {
+    const dim3 grid((unsigned) p.T, (unsigned) ((p.H + 3) / 4));
+    if (cache) hipLaunchKernelGGL((norm_rope_kernel<MODE, true>), grid, dim3(256), 0, stream, p);
+    else       hipLaunchKernelGGL((norm_rope_kernel<MODE, false>), grid, dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+// YaRN correction dimension for a rotation count (ops.cpp:728-730).
+float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
+    const double pi = 3.14159265358979323846;
+    return n_dims * logf(n_ctx_orig / (n_rot * 2 * (float) pi)) / (2 * logf(base));
+}
+
+}  // namespace
+
+extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
+                                    const al_rope_params * rope, const al_tensor * y, const al_tensor * rows,
+                                    void * stream) {
+    if (!x || !pos || !y) return al_fail(AL_ERR_INVALID, "rms_norm_rope: x, pos and y required");
+    if (x->type != AL_TYPE_F32 || x->ne[0] != 128 || x->nb[0] != 4 || x->ne[3] != 1)
+        return al_fail(AL_ERR_UNSUPPORTED, "rms_norm_rope: x must be f32 [128, H, T, 1] with nb0 = 4");
+    const int64_t H = x->ne[1], T = x->ne[2];
+    if (H <= 0 || T <= 0 || T > INT32_MAX / 2 || H > 65535 * 4) return al_fail(AL_ERR_INVALID, "rms_norm_rope: bad H %lld or T %lld", (long long) H, (long long) T);
+    if (!(eps >= 0.0f)) return al_fail(AL_ERR_INVALID, "rms_norm_rope: eps %g < 0 (ops.cpp:697)", (double) eps);
+    if (w && (w->type != AL_TYPE_F32 || w->ne[0] < 128 || w->nb[0] != 4 || !w->data))
+        return al_fail(AL_ERR_INVALID, "rms_norm_rope: w must be f32 [128]");
+    if (pos->type != AL_TYPE_I32 || pos->ne[0] != T || pos->nb[0] != 4 || !pos->data)
+        return al_fail(AL_ERR_INVALID, "rms_norm_rope: pos must be i32 [T] (tensor.cpp:1014-1019)");
+    int mode = 0;
+    NormRopeParams p;
+    memset(&p, 0, sizeof(p));
+    if (rope) {
+        if (rope->n_dims != 128) return al_fail(AL_ERR_UNSUPPORTED, "rms_norm_rope: n_dims %d (only the full head, 128)", rope->n_dims);
+        if (rope->mode == AL_ROPE_NEOX) mode = 2;
+        else if (rope->mode == AL_ROPE_NORMAL) mode = 1;
+        else return al_fail(AL_ERR_UNSUPPORTED, "rms_norm_rope: rope mode %d", rope->mode);
+        // host-side constants exactly as the reference's rope op computes them
+        p.theta_scale = powf(rope->freq_base, -2.0f / rope->n_dims);
+        const float start = floorf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_fast, rope->freq_base));
+        const float end = ceilf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_slow, rope->freq_base));
+        p.corr0 = fmaxf(0.0f, start);
+        p.corr1 = fminf((float) (rope->n_dims - 1), end);
+        p.freq_scale = rope->freq_scale;
+        p.ext_factor = rope->ext_factor;
+        p.mscale = rope->attn_factor;
+        if (rope->ext_factor != 0.0f) p.mscale *= 1.0f + 0.1f * logf(1.0f / rope->freq_scale);
+    }
+    p.x = (const char *) x->data; p.x_nb1 = (int64_t) x->nb[1]; p.x_nb2 = (int64_t) x->nb[2];
+    p.w = w ? (const float *) w->data : nullptr;
+    p.pos = (const int32_t *) pos->data;
+    p.H = (int32_t) H; p.T = (int32_t) T;
+    p.eps = eps;
+    const bool cache = rows != nullptr;
+    if (cache) {
+        if (y->type != AL_TYPE_F16 || y->ne[0] != 128 * H || y->nb[0] != 2 || (int64_t) y->nb[1] < 256 * H)
+            return al_fail(AL_ERR_INVALID, "rms_norm_rope: cache must be f16 [128*H, n_rows] with contiguous rows");
+        if ((rows->type != AL_TYPE_I64 && rows->type != AL_TYPE_I32) || rows->ne[0] != T || !rows->data)
+            return al_fail(AL_ERR_INVALID, "rms_norm_rope: rows must be i64 / i32 [T]");
+        p.rows = (const char *) rows->data;
+        p.rows_nb0 = (int64_t) rows->nb[0];
+        p.rows64 = rows->type == AL_TYPE_I64;
+        p.n_rows_dst = y->ne[1];
+        p.y_nb1 = (int64_t) y->nb[1];
+        int rc = al_device_error_flag(&p.err);
+        if (rc != AL_OK) return rc;
+    } else {
+        if (y->type != AL_TYPE_F32 || y->ne[0] != 128 || y->ne[1] != H || y->ne[2] != T || y->nb[0] != 4)
+            return al_fail(AL_ERR_INVALID, "rms_norm_rope: y must be f32 [128, H, T] with nb0 = 4");
+        p.y_nb1 = (int64_t) y->nb[1];
+        p.y_nb2 = (int64_t) y->nb[2];
+    }
+    p.y = (char *) y->data;
+    if (!p.x || !p.y) return al_fail(AL_ERR_INVALID, "rms_norm_rope: null data");
+    hipStream_t s = (hipStream_t) stream;
+    hipError_t e;
+    switch (mode) {
+        case 2: e = launch_mode<2>(p, cache, s); break;
+        case 1: e = launch_mode<1>(p, cache, s); break;
+        default: e = launch_mode<0>(p, cache, s); break;
+    }
+    return e == hipSuccess ? AL_OK : al_hip_fail(e, "rms_norm_rope: launch");
+}

@@ -166,6 +166,21 @@ class KvRing:
     def get_v(self, il, n_kv, s0=0, ns=None):
         return self._view("al_kv_ring_view_v", il, n_kv, s0, ns)
 
+    def cache_rows(self, il, which="k"):
+        """Layer il's whole K or V cache as rows of one cell (all kv heads):
+        f16 ne = [n_head_kv*head_dim, kv_size*n_stream], the destination
+        the cpy_k / cpy_v set_rows write (cgraph.cpp:1114-1180)."""
+        full = self.get_k(il, self.params.kv_size) if which == "k" else self.get_v(il, self.params.kv_size)
+        t = abi.AlTensor()
+        t.data = full.ptr
+        t.type = abi.AL_TYPE_F16
+        nc = self.params.n_head_kv * self.params.head_dim
+        rows = self.params.kv_size * self.n_stream
+        for i, (ne, nb) in enumerate(((nc, 2), (rows, nc * 2), (1, nc * 2 * rows), (1, nc * 2 * rows))):
+            t.ne[i] = ne
+            t.nb[i] = nb
+        return _RawView(t)
+
     def cpy_kv(self, il, k_cur, v_cur, rows, stream=None):
         """Writes f32 rows [n_tokens, n_head_kv*head_dim] (DeviceTensors) at
         cache rows `rows` (DeviceTensor int64 [n_tokens])."""

@@ -13,6 +13,9 @@
  *   nnml/include/ops.h:276-323          IEEE fp16 conversions (RNE)
  *   nnml/src/ops/ops.cpp:135-181        set_rows f32 -> f16
  *   nnml/src/tensor.cpp:1292-1338       operand preconditions
+ *   nnml/src/ops/ops.cpp:680-726        rms_norm f32 (squares summed in double)
+ *   nnml/src/ops/ops.cpp:728-777        rope_yarn, rotation cache, YaRN corr dims
+ *   nnml/src/ops/ops.cpp:871-962        rope f32 (NEOX and normal pairs)
  *
  * Pinning (tests/test_oracle_*.py): the fp16 conversions are compared bit
  * for bit with numpy's IEEE conversions over every f16 pattern and millions
@@ -401,5 +404,96 @@ int orc_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src, const al_
                 uint16_t * d = (uint16_t *) ((char *) dst->data + i1 * dst->nb[1] + i02 * dst->nb[2] + i03 * dst->nb[3]);
                 for (int64_t c = 0; c < nc; ++c) d[c] = orc_f32_to_f16(s[c]);
             }
+    return AL_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* Attention-operand producers: RMSNorm, weight, rotary embedding      */
+/* ------------------------------------------------------------------ */
+
+/* YaRN correction dimension for a rotation count (ops.cpp:728-730). */
+static float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
+    const double pi = 3.14159265358979323846;   /* M_PI */
+    return n_dims * logf(n_ctx_orig / (n_rot * 2 * (float) pi)) / (2 * logf(base));
+}
+
+/* Rotation angle of pair index i0 / 2 and its cos / sin with the YaRN
+ * extrapolation mix and magnitude correction (ops.cpp:743-760). */
+static void yarn_cos_sin(float theta_extrap, float freq_scale, const float corr[2], int64_t i0, float ext_factor,
+                         float mscale, float * c, float * s) {
+    const float theta_interp = freq_scale * theta_extrap;
+    float theta = theta_interp;
+    if (ext_factor != 0.0f) {
+        const float y = (float) (i0 / 2 - corr[0]) / fmaxf(0.001f, corr[1] - corr[0]);
+        const float ramp = 1 - fminf(1, fmaxf(0, y));
+        const float mix = ramp * ext_factor;
+        theta = theta_interp * (1 - mix) + theta_extrap * mix;
+        mscale *= 1.0f + 0.1f * logf(1.0f / freq_scale);
+    }
+    *c = cosf(theta) * mscale;
+    *s = sinf(theta) * mscale;
+}
+
+int orc_rms_norm_rope_f32(const float * x, const float * w, const int32_t * pos, int64_t T, int64_t H, int64_t D,
+                          float eps, const al_rope_params * rope, float * y) {
+    if (D <= 0 || D % 2 != 0 || eps < 0.0f) return AL_ERR_INVALID;
+    if (rope && (rope->n_dims != D || (rope->mode != AL_ROPE_NEOX && rope->mode != AL_ROPE_NORMAL))) return AL_ERR_UNSUPPORTED;
+    float * cs = malloc(sizeof(float) * (size_t) D);
+    if (!cs) return AL_ERR_INVALID;
+    float corr[2] = {0, 0};
+    float theta_scale = 1.0f;
+    if (rope) {
+        theta_scale = powf(rope->freq_base, -2.0f / rope->n_dims);
+        const float start = floorf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_fast, rope->freq_base));
+        const float end = ceilf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_slow, rope->freq_base));
+        corr[0] = fmaxf(0, start);
+        corr[1] = fminf(rope->n_dims - 1, end);
+    }
+    for (int64_t t = 0; t < T; ++t) {
+        if (rope) {
+            /* the rotation cache of this position: the angle is carried from
+             * pair to pair by repeated multiplication (ops.cpp:762-772) */
+            float theta = (float) pos[t];
+            for (int64_t i0 = 0; i0 < D; i0 += 2) {
+                yarn_cos_sin(theta, rope->freq_scale, corr, i0, rope->ext_factor, rope->attn_factor, &cs[i0], &cs[i0 + 1]);
+                theta *= theta_scale;
+            }
+        }
+        for (int64_t h = 0; h < H; ++h) {
+            const float * xr = x + (t * H + h) * D;
+            float * yr = y + (t * H + h) * D;
+            /* RMSNorm: squares summed in double, scale in float (ops.cpp:700-722) */
+            double sum = 0.0;
+            for (int64_t i = 0; i < D; ++i) sum += (double) (xr[i] * xr[i]);
+            const float mean = (float) (sum / D);
+            const float scale = 1.0f / sqrtf(mean + eps);
+            float * n = malloc(sizeof(float) * (size_t) D);
+            if (!n) { free(cs); return AL_ERR_INVALID; }
+            for (int64_t i = 0; i < D; ++i) {
+                n[i] = xr[i] * scale;
+                if (w) n[i] = n[i] * w[i];
+            }
+            if (!rope) {
+                memcpy(yr, n, sizeof(float) * (size_t) D);
+            } else if (rope->mode == AL_ROPE_NEOX) {
+                const int64_t half = D / 2;
+                for (int64_t ic = 0; ic < half; ++ic) {
+                    const float c = cs[2 * ic], s = cs[2 * ic + 1];
+                    const float x0 = n[ic], x1 = n[ic + half];
+                    yr[ic] = x0 * c - x1 * s;
+                    yr[ic + half] = x0 * s + x1 * c;
+                }
+            } else {
+                for (int64_t i0 = 0; i0 < D; i0 += 2) {
+                    const float c = cs[i0], s = cs[i0 + 1];
+                    const float x0 = n[i0], x1 = n[i0 + 1];
+                    yr[i0] = x0 * c - x1 * s;
+                    yr[i0 + 1] = x0 * s + x1 * c;
+                }
+            }
+            free(n);
+        }
+    }
+    free(cs);
     return AL_OK;
 }

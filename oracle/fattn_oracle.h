@@ -25,6 +25,7 @@
 
 #include <stdint.h>
 #include "../include/arclight_fattn.h"
+#include "../include/arclight_prologue.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -45,6 +46,15 @@ int orc_fattn_o3(const al_fattn_args * a, int n_threads);
 /* set_rows f32 -> f16 (nnml/src/ops/ops.cpp:135-181). */
 int orc_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
                          const al_tensor * idx);
+
+/* The attention-operand producers of the Qwen3 layer, host memory:
+ * y = rope(rms_norm(x) * w) over rows of D floats; x, y f32 [T][H][D]
+ * contiguous, w [D] or NULL, pos [T], rope NULL for no rotation. Restates
+ * nnml_compute_forward_rms_norm_f32 (ops.cpp:680-726), the f32 mul, and
+ * nnml_compute_forward_rope_f32 (ops.cpp:871-962) with rope_yarn, the
+ * rotation cache and the YaRN correction dims (ops.cpp:728-777). */
+int orc_rms_norm_rope_f32(const float * x, const float * w, const int32_t * pos, int64_t T, int64_t H, int64_t D,
+                          float eps, const al_rope_params * rope, float * y);
 
 #ifdef __cplusplus
 }

@@ -45,6 +45,9 @@ def lib():
             f.argtypes = [ctypes.POINTER(abi.AlFattnArgs), ctypes.c_int]
         L.orc_set_rows_f32_f16.restype = ctypes.c_int
         L.orc_set_rows_f32_f16.argtypes = [ctypes.POINTER(abi.AlTensor)] * 3
+        L.orc_rms_norm_rope_f32.restype = ctypes.c_int
+        L.orc_rms_norm_rope_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
+            ctypes.c_float, ctypes.POINTER(abi.AlRopeParams), ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -163,3 +166,18 @@ def causal_mask(T, n_kv, pos0, kv_len=None, n_stream=1):
         vis = (c < kv_len) & (c <= pos0 + t)
         m[:, 0, t, vis] = 0.0
     return m
+
+
+def rms_norm_rope(x, w=None, pos=None, *, eps=1e-6, rope=None):
+    """Oracle of the Q/K producers: rope(rms_norm(x) * w) with x (T, H, D) f32,
+    w (D,) or None, pos (T,) int32, rope an AlRopeParams or None."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H, D = x.shape
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    pos = np.zeros(T, np.int32) if pos is None else np.ascontiguousarray(pos, dtype=np.int32)
+    y = np.empty_like(x)
+    rc = lib().orc_rms_norm_rope_f32(x.ctypes.data, None if w is None else w.ctypes.data, pos.ctypes.data, T, H, D,
+                                     eps, ctypes.byref(rope) if rope is not None else None, y.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"oracle rms_norm_rope rejected the operands: {abi.STATUS_NAMES.get(rc, rc)}")
+    return y
