@@ -10,6 +10,7 @@ import ctypes
 
 AL_TYPE_F32 = 0
 AL_TYPE_F16 = 1
+AL_TYPE_Q4_0 = 2     # include/arclight_matmul.h
 AL_TYPE_I32 = 26
 AL_TYPE_I64 = 27
 
@@ -31,6 +32,11 @@ STATUS_NAMES = {
 }
 
 TYPE_SIZES = {AL_TYPE_F32: 4, AL_TYPE_F16: 2, AL_TYPE_I32: 4, AL_TYPE_I64: 8}
+
+# Q4_0 blocks (nnml/include/nnml.h:646-650): 32 weights as an f16 scale and
+# 16 bytes of nibbles, low nibbles the first 16 weights (types.cpp:337-350).
+QK4_0 = 32
+Q4_0_BLOCK_BYTES = 18
 
 
 class AlTensor(ctypes.Structure):

@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the 4K/16K decode, 8K verify and Qwen3-32B-shape lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
-    ap.add_argument("--only", choices=["decode", "prefill", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "wo", "copy"], default=None,
                     help="run one workload only (for profiling); prints its own JSON line")
     return ap.parse_args()
 
@@ -87,14 +87,16 @@ def run_calls(lib, arg_list):
             raise RuntimeError(lib.al_last_error().decode())
 
 
-def time_graph(lib, stream, arg_list, steps, warmup):
-    """Captures one step into a HIP graph; returns (ms_per_step, graph_exec)."""
+def time_graph(lib, stream, arg_list, steps, warmup, enqueue=None):
+    """Captures one step (the attention calls of arg_list, or enqueue())
+    into a HIP graph and replays it; returns ms per step."""
     from arclight_amd import device
     from arclight_amd._lib import call
-    run_calls(lib, arg_list)                      # allocates the workspace outside the capture
+    enqueue = enqueue or (lambda: run_calls(lib, arg_list))
+    enqueue()                                     # allocates workspaces outside the capture
     stream.synchronize()
     call("al_util_graph_begin", stream.handle)
-    run_calls(lib, arg_list)
+    enqueue()
     ge = ctypes.c_void_p()
     call("al_util_graph_end", stream.handle, ctypes.byref(ge))
     for _ in range(warmup):
@@ -180,7 +182,8 @@ def bench_other_configs(lib, stream, a):
     at 4K and 16K, speculative verify at 8K context with 4 and 8 drafts
     (Qwen3-8B attention shape = Qwen3-4B's), and the Qwen3-32B shape (64
     query heads, 64 layers) for decode at 32K and 4096-token prefill in
-    1024-token chunks."""
+    1024-token chunks; then the attention output projection (Q4_0 WO) that
+    consumes the attention output, for decode and an 8-token verify."""
     out = []
     steps = max(2, a.steps // 2)
 
@@ -202,7 +205,46 @@ def bench_other_configs(lib, stream, a):
                 "mfma_peak_frac": round(r["tflops"] / F16_PEAK_TFLOPS, 4),
                 "us_per_launch": round(r["kernel_ms_mean"] * 1e3, 2)})
     print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
+    for name, K, N, T in [("WO projection Q4_0, Qwen3-4B shape (4096 -> 2560), 1 token", 4096, 2560, 1),
+                          ("WO projection Q4_0, Qwen3-4B shape (4096 -> 2560), 8 tokens", 4096, 2560, 8),
+                          ("WO projection Q4_0, Qwen3-32B shape (8192 -> 5120), 1 token", 8192, 5120, 1)]:
+        r = bench_wo(lib, stream, a, K=K, N=N, T=T, copies=64 if K == 4096 else 16, steps=steps)
+        out.append({"workload": name, "value": round(r["gbs"], 1), "unit": "GB/s",
+                    "hbm_peak_frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                    "us_per_op": round(r["op_ms_mean"] * 1e3, 2)})
+        print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
     return out
+
+
+def wo_bytes(K, N, T):
+    """Algorithmic bytes of one WO projection: the Q4_0 weights (18 bytes
+    per 32), the f32 activations read and the f32 outputs written."""
+    return N * K // 32 * 18 + T * K * 4 + T * N * 4
+
+
+def bench_wo(lib, stream, a, K=4096, N=2560, T=1, copies=64, steps=None):
+    """The attention output projection with Q4_0 weights: each step runs it
+    once on each of `copies` distinct weight matrices (together larger than
+    the 256 MB last-level cache, so every launch streams its weights from
+    HBM), as L layers would."""
+    from arclight_amd import device, matmul
+    rng = np.random.default_rng(a.seed + 7)
+    nb = K // 32
+    blocks = np.empty((N, nb, 18), np.uint8)
+    blocks[:] = rng.integers(0, 256, size=(N, nb, 18), dtype=np.uint8)
+    blocks[:, :, :2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+    ws = [matmul.Q4_0Matrix(blocks, K, N) for _ in range(copies)]
+    x = device.DeviceTensor.from_numpy(rng.standard_normal((T, K)).astype(np.float32))
+    y = device.DeviceTensor.empty((T, N), np.float32)
+
+    def enqueue():
+        for w in ws:
+            matmul.mul_mat_q4_0(w, x, y, stream)
+
+    ms = time_graph(lib, stream, None, steps or a.steps, a.warmup, enqueue)
+    byts = wo_bytes(K, N, T)
+    return {"ms_per_step": ms, "bytes_per_launch": byts, "gbs": byts * copies / (ms * 1e-3) / 1e9,
+            "op_ms_mean": ms / copies}
 
 
 def bench_copy(stream, nbytes=1 << 30):
@@ -282,6 +324,9 @@ def main():
         return
     if a.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(lib, stream, a)}))
+        return
+    if a.only == "wo":
+        print(json.dumps({"wo": bench_wo(lib, stream, a)}))
         return
 
     dec = bench_decode(lib, stream, a)

@@ -16,6 +16,9 @@
  *   nnml/src/ops/ops.cpp:680-726        rms_norm f32 (squares summed in double)
  *   nnml/src/ops/ops.cpp:728-777        rope_yarn, rotation cache, YaRN corr dims
  *   nnml/src/ops/ops.cpp:871-962        rope f32 (NEOX and normal pairs)
+ *   nnml/src/ops/arm/arm.cpp:1819-1848  quantize_row_q8_0 (NEON: round to nearest even)
+ *   nnml/src/ops/arm/arm.cpp:401-...    vec_dot_q4_0_q8_0 (scalar path)
+ *   nnml/src/ops/arm/common.cpp:120-... forward_mul_mat_generic
  *
  * Pinning (tests/test_oracle_*.py): the fp16 conversions are compared bit
  * for bit with numpy's IEEE conversions over every f16 pattern and millions
@@ -495,5 +498,48 @@ int orc_rms_norm_rope_f32(const float * x, const float * w, const int32_t * pos,
         }
     }
     free(cs);
+    return AL_OK;
+}
+
+/* ------------------------------------------------------------------ */
+/* Q4_0 x Q8_0 matrix product (the WO projection)                       */
+/* ------------------------------------------------------------------ */
+
+void orc_quantize_row_q8_0(const float * x, orc_block_q8_0 * y, int64_t k) {
+    for (int64_t b = 0; b < k / 32; ++b) {
+        const float * xb = x + 32 * b;
+        float amax = 0.0f;
+        for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(xb[j]));
+        const float d = amax / 127;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[b].d = orc_f32_to_f16(d);
+        for (int j = 0; j < 32; ++j) y[b].qs[j] = (int8_t) nearbyintf(xb[j] * id);   /* ties to even */
+    }
+}
+
+float orc_vec_dot_q4_0_q8_0(int64_t n, const orc_block_q4_0 * x, const orc_block_q8_0 * y) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < n / 32; ++b) {
+        int lo = 0, hi = 0;
+        for (int j = 0; j < 16; ++j) {
+            lo += ((x[b].qs[j] & 0x0F) - 8) * y[b].qs[j];
+            hi += ((x[b].qs[j] >> 4) - 8) * y[b].qs[j + 16];
+        }
+        const int sumi = lo + hi;
+        sumf += sumi * orc_f16_to_f32(x[b].d) * orc_f16_to_f32(y[b].d);
+    }
+    return sumf;
+}
+
+int orc_mul_mat_q4_0_f32(const void * w, int64_t K, int64_t N, const float * x, int64_t T, float * y) {
+    if (K <= 0 || K % 32 != 0 || N <= 0 || T <= 0) return AL_ERR_INVALID;
+    const int64_t nb = K / 32;
+    orc_block_q8_0 * q = malloc(sizeof(orc_block_q8_0) * (size_t) (nb * T));
+    if (!q) return AL_ERR_INVALID;
+    for (int64_t t = 0; t < T; ++t) orc_quantize_row_q8_0(x + t * K, q + t * nb, K);
+    const orc_block_q4_0 * wb = (const orc_block_q4_0 *) w;
+    for (int64_t t = 0; t < T; ++t)
+        for (int64_t r = 0; r < N; ++r) y[t * N + r] = orc_vec_dot_q4_0_q8_0(K, wb + r * nb, q + t * nb);
+    free(q);
     return AL_OK;
 }

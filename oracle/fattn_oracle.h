@@ -56,6 +56,20 @@ int orc_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
 int orc_rms_norm_rope_f32(const float * x, const float * w, const int32_t * pos, int64_t T, int64_t H, int64_t D,
                           float eps, const al_rope_params * rope, float * y);
 
+/* Q4_0 / Q8_0 blocks (nnml/include/nnml.h:646-650, 695-699). */
+typedef struct { uint16_t d; uint8_t qs[16]; } orc_block_q4_0;
+typedef struct { uint16_t d; int8_t qs[32]; } orc_block_q8_0;
+
+/* quantize_row_q8_0 as the NEON build runs it (arm.cpp:1819-1848): per
+ * block of 32, d = amax / 127, q = round-to-nearest-even(x / d). */
+void orc_quantize_row_q8_0(const float * x, orc_block_q8_0 * y, int64_t k);
+/* nnml_vec_dot_q4_0_q8_0, scalar path (arm.cpp:401-...): sum over blocks of
+ * sumi * d_x * d_y in float, blocks in order. */
+float orc_vec_dot_q4_0_q8_0(int64_t n, const orc_block_q4_0 * x, const orc_block_q8_0 * y);
+/* mul_mat with Q4_0 weights w [N][K/32 blocks] and f32 activations
+ * x [T][K]: y [T][N] (forward_mul_mat_generic, common.cpp:120-...). */
+int orc_mul_mat_q4_0_f32(const void * w, int64_t K, int64_t N, const float * x, int64_t T, float * y);
+
 #ifdef __cplusplus
 }
 #endif

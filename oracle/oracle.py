@@ -48,6 +48,13 @@ def lib():
         L.orc_rms_norm_rope_f32.restype = ctypes.c_int
         L.orc_rms_norm_rope_f32.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] * 3 + [
             ctypes.c_float, ctypes.POINTER(abi.AlRopeParams), ctypes.c_void_p]
+        L.orc_quantize_row_q8_0.restype = None
+        L.orc_quantize_row_q8_0.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
+        L.orc_vec_dot_q4_0_q8_0.restype = ctypes.c_float
+        L.orc_vec_dot_q4_0_q8_0.argtypes = [ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_mul_mat_q4_0_f32.restype = ctypes.c_int
+        L.orc_mul_mat_q4_0_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_int64, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -180,4 +187,52 @@ def rms_norm_rope(x, w=None, pos=None, *, eps=1e-6, rope=None):
                                      eps, ctypes.byref(rope) if rope is not None else None, y.ctypes.data)
     if rc != 0:
         raise ValueError(f"oracle rms_norm_rope rejected the operands: {abi.STATUS_NAMES.get(rc, rc)}")
+    return y
+
+
+# Q4_0 / Q8_0 blocks as numpy records (nnml/include/nnml.h:646-650, 695-699).
+Q4_0 = np.dtype([("d", "<u2"), ("qs", "u1", 16)])
+Q8_0 = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
+
+
+def random_q4_0(rng, N, K, scale=0.02):
+    """N rows of K / 32 Q4_0 blocks: uniform nibbles and f16 scales of both
+    signs (quantize_row_q4_0_ref stores d = max / -8, types.cpp:352-377)."""
+    w = np.empty((N, K // 32), dtype=Q4_0)
+    w["qs"] = rng.integers(0, 256, size=(N, K // 32, 16), dtype=np.uint8)
+    d = (rng.uniform(0.25, 1.0, size=(N, K // 32)) * scale * rng.choice([-1.0, 1.0], size=(N, K // 32)))
+    w["d"] = d.astype(np.float16).view(np.uint16)
+    return w
+
+
+def quantize_q8_0(x):
+    """quantize_row_q8_0 over each row of x (T, K) f32: (T, K / 32) Q8_0."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, K = x.shape
+    y = np.empty((T, K // 32), dtype=Q8_0)
+    for t in range(T):
+        lib().orc_quantize_row_q8_0(x[t].ctypes.data, y[t].ctypes.data, K)
+    return y
+
+
+def vec_dot_q4_0_q8_0(wrow, qrow):
+    """One Q4_0 row (K / 32 blocks) dotted with one Q8_0 row."""
+    wrow = np.ascontiguousarray(wrow, dtype=Q4_0)
+    qrow = np.ascontiguousarray(qrow, dtype=Q8_0)
+    return float(lib().orc_vec_dot_q4_0_q8_0(32 * wrow.size, wrow.ctypes.data, qrow.ctypes.data))
+
+
+def mul_mat_q4_0(w, x):
+    """Oracle of the WO projection: w (N, K / 32) Q4_0, x (T, K) f32 ->
+    y (T, N) f32, y[t, n] the dot product of row n with quantized row t."""
+    w = np.ascontiguousarray(w, dtype=Q4_0)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    N, nb = w.shape
+    T, K = x.shape
+    if K != 32 * nb:
+        raise ValueError(f"mul_mat_q4_0: w has {nb} blocks per row, x has {K} columns")
+    y = np.empty((T, N), dtype=np.float32)
+    rc = lib().orc_mul_mat_q4_0_f32(w.ctypes.data, K, N, x.ctypes.data, T, y.ctypes.data)
+    if rc != 0:
+        raise ValueError(f"oracle mul_mat_q4_0 rejected the operands: {abi.STATUS_NAMES.get(rc, rc)}")
     return y
