@@ -165,13 +165,50 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const char * __restrict__ 
     }
 }
 
-// One launch for decode and verify: every workgroup issues its rows' weight
-// loads, quantizes all T activation rows into LDS meanwhile (they are small
-// and L2-resident after the first workgroup touches them), then runs the
-// dot products of gemv_q4_kernel from LDS. One wavefront per row.
-template <int BPL>
-__global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * __restrict__ w, int64_t w_nb1, int N, int K,
-                                                             const char * __restrict__ x, int64_t x_nb1, int T,
+// Eight values of a Q8_0 block (part 0..3 of it, the four parts in the four
+// lanes of a quad) quantized into LDS.
+__device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, const int part, int8_t * qdst,
+                                              float * ddst, int * sdst) {
+    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+    amax = fmaxf(amax, dpp<kQuadXor1>(amax));
+    amax = fmaxf(amax, dpp<kQuadXor2>(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    int sum = 0;
+    uint32_t words[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int q = (int) rintf(v[4 * j + k] * id);                // ties to even, as vcvtnq
+            sum += q;
+            wv |= (uint32_t) (q & 0xff) << (8 * k);
+        }
+        words[j] = wv;
+    }
+    float fs = (float) sum;                                             // |sum| <= 1016: exact in f32
+    fs += dpp<kQuadXor1>(fs);
+    fs += dpp<kQuadXor2>(fs);
+    *(uint2 *) qdst = uint2{words[0], words[1]};
+    if (part == 0) {
+        *ddst = (float) (_Float16) d;                                   // the block scale as stored (f16)
+        *sdst = (int) fs;
+    }
+}
+
+// One launch for decode and verify (T <= TMAX): every workgroup issues its
+// rows' weight loads, quantizes all T activation rows into LDS meanwhile
+// (they are small and L2-resident after the first workgroup touches them;
+// each thread issues the loads of all T tokens of its part of a block before
+// using any), then runs the dot products of gemv_q4_kernel from LDS. One
+// wavefront per row.
+template <int BPL, int TMAX>
+__global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int64_t w_nb1, int N, int K,
+                                                             const char * x, int64_t x_nb1, int T,
                                                              char * __restrict__ y, int64_t y_nb1) {
     extern __shared__ __align__(16) char lds[];
     const int nb = K / 32;
@@ -182,48 +219,55 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * __rest
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int b0 = lane * BPL;
 
+    // (block, part) items of the activations, a uniform number of rounds per
+    // thread; loads are unconditional (indices clamped in bounds) so that no
+    // branch makes the compiler wait for outstanding loads early
+    const int items = 4 * nb;
+    const int rounds = (items + blockDim.x - 1) / blockDim.x;
+    constexpr int PRE = TMAX == 1 ? 2 : 1;                             // rounds whose loads go out first
+    float4 f[PRE][TMAX][2];
+    // LDS holds block b at slot (b % BPL) * 64 + b / BPL, so that the dot
+    // products' reads (lane l, its j-th block) are lane-consecutive; item i
+    // is part i % 4 of the block in slot i / 4
+    auto block_at = [](const int slot) { return (slot & 63) * BPL + (slot >> 6); };
+    auto load_item = [&](const int item, float4 (&g)[TMAX][2]) {
+        const int it = item < items ? item : items - 1;
+        const int b = block_at(it >> 2), part = it & 3;
+#pragma unroll
+        for (int t = 0; t < TMAX; ++t) {                                // rows past T re-read row T-1
+            const int tr = t < T ? t : T - 1;
+            const float4 * xb = (const float4 *) ((const float *) (x + (int64_t) tr * x_nb1) + 32 * b + 8 * part);
+            g[t][0] = xb[0];
+            g[t][1] = xb[1];
+        }
+    };
+    auto quantize_item = [&](const int item, const float4 (&g)[TMAX][2]) {
+        if (item < items) {
+            const int sl = item >> 2, part = item & 3;
+#pragma unroll
+            for (int t = 0; t < TMAX; ++t)
+                if (t < T) quantize_part(g[t][0], g[t][1], part, qs + t * K + 32 * sl + 8 * part, dx + t * nb + sl, sy + t * nb + sl);
+        }
+    };
+    // the first rounds' activations (L2) before the weights (HBM): the
+    // quantization then waits only for the former
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) load_item(threadIdx.x + k * blockDim.x, f[k]);
+    asm volatile("" ::: "memory");                                     // keeps the issue order
     uint32_t c[9 * BPL / 2];
-    if (row < N) {
-        const uint32_t * wr = (const uint32_t *) (w + (int64_t) row * w_nb1 + (int64_t) b0 * 18);
+    {
+        const int r = row < N ? row : N - 1;
+        const uint32_t * wr = (const uint32_t *) (w + (int64_t) r * w_nb1 + (int64_t) b0 * 18);
 #pragma unroll
-        for (int i = 0; i < 9 * BPL / 2; ++i) c[i] = wr[i];
+        for (int i = 0; i < 9 * BPL / 2; ++i) c[i] = wr[i];           // (non-temporal loads measured slower)
     }
-
-    // four lanes of a quad per block, eight values each
-    for (int i = threadIdx.x; i < 4 * T * nb; i += blockDim.x) {
-        const int blk = i >> 2, part = i & 3;
-        const int t = blk / nb, b = blk % nb;
-        const float4 * xb = (const float4 *) ((const float *) (x + (int64_t) t * x_nb1) + 32 * b + 8 * part);
-        const float4 f0 = xb[0], f1 = xb[1];
-        const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-        float amax = 0.0f;
+    asm volatile("" ::: "memory");
 #pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
-        amax = fmaxf(amax, dpp<kQuadXor1>(amax));
-        amax = fmaxf(amax, dpp<kQuadXor2>(amax));
-        const float d = amax / 127.0f;
-        const float id = d != 0.0f ? 1.0f / d : 0.0f;
-        int sum = 0;
-        uint32_t words[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            uint32_t wv = 0;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int q = (int) rintf(v[4 * j + k] * id);
-                sum += q;
-                wv |= (uint32_t) (q & 0xff) << (8 * k);
-            }
-            words[j] = wv;
-        }
-        float fs = (float) sum;                                         // |sum| <= 1016: exact in f32
-        fs += dpp<kQuadXor1>(fs);
-        fs += dpp<kQuadXor2>(fs);
-        *(uint2 *) (qs + t * K + 32 * b + 8 * part) = uint2{words[0], words[1]};
-        if (part == 0) {
-            dx[blk] = (float) (_Float16) d;
-            sy[blk] = (int) fs;
-        }
+    for (int k = 0; k < PRE; ++k)
+        if (k < rounds) quantize_item(threadIdx.x + k * blockDim.x, f[k]);
+    for (int k = PRE; k < rounds; ++k) {
+        load_item(threadIdx.x + k * blockDim.x, f[0]);
+        quantize_item(threadIdx.x + k * blockDim.x, f[0]);
     }
     __syncthreads();
     if (row >= N) return;
@@ -244,8 +288,8 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * __rest
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < BPL; ++j) {
-            const int b = b0 + j;
-            const uint4 * ab = (const uint4 *) (qs + t * K + 32 * b);
+            const int sl = j * 64 + lane;                                // block b0 + j
+            const uint4 * ab = (const uint4 *) (qs + t * K + 32 * sl);
             const uint4 a0 = ab[0], a1 = ab[1];
             const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             int dot = 0;
@@ -254,35 +298,43 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * __rest
                 dot = __builtin_amdgcn_sdot4((int) lo[j][i], (int) a[i], dot, false);
                 dot = __builtin_amdgcn_sdot4((int) hi[j][i], (int) a[4 + i], dot, false);
             }
-            const int sumi = dot - 8 * sy[t * nb + b];
-            part += ((float) sumi * dw[j]) * dx[t * nb + b];
+            const int sumi = dot - 8 * sy[t * nb + sl];
+            part += ((float) sumi * dw[j]) * dx[t * nb + sl];
         }
         part = wave_sum_to_last(part);
         if (lane == 63) *(float *) (y + (int64_t) t * y_nb1 + (int64_t) row * 4) = part;
     }
 }
 
-constexpr size_t kFusedLds = 160 * 1024;
+constexpr int kFusedMaxT = 8;
 
-size_t fused_lds_bytes(int64_t K, int64_t T) { return (size_t) (T * K + 8 * T * (K / 32)); }
+size_t fused_lds_bytes(int64_t K, int64_t T) { return (size_t) (T * K + 8 * T * (K / 32)); }   // <= 160 KiB
 
-template <int BPL>
+template <int BPL, int TMAX>
 int launch_fused(const al_tensor * w, const al_tensor * x, const al_tensor * y, int N, int K, int T, hipStream_t st) {
     int n_cu = 0;
     int rc = al_device_cu_count(&n_cu);
     if (rc != AL_OK) return rc;
-    const int waves = std::min(16, std::max(1, (N + n_cu - 1) / n_cu));
+    // one wavefront per row, all rows resident at once: the fewest workgroups
+    // per CU that keep a workgroup at 16 waves or fewer
+    const int per_cu = (N + 16 * n_cu - 1) / (16 * n_cu);
+    const int waves = std::max(1, (N + per_cu * n_cu - 1) / (per_cu * n_cu));
     const size_t lds = fused_lds_bytes(K, T);
     if (lds > 64 * 1024) {
-        hipError_t e = hipFuncSetAttribute((const void *) gemv_q4_fused_kernel<BPL>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           (int) kFusedLds);
+        hipError_t e = hipFuncSetAttribute((const void *) gemv_q4_fused_kernel<BPL, TMAX>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int) lds);
         if (e != hipSuccess) return al_hip_fail(e, "mul_mat_q4_0: LDS attribute");
     }
-    hipLaunchKernelGGL(gemv_q4_fused_kernel<BPL>, dim3((unsigned) ((N + waves - 1) / waves)), dim3(64 * waves), lds, st,
+    hipLaunchKernelGGL((gemv_q4_fused_kernel<BPL, TMAX>), dim3((unsigned) ((N + waves - 1) / waves)), dim3(64 * waves), lds, st,
                        (const char *) w->data, (int64_t) w->nb[1], N, K, (const char *) x->data, (int64_t) x->nb[1], T,
                        (char *) y->data, (int64_t) y->nb[1]);
     hipError_t e = hipGetLastError();
     return e == hipSuccess ? AL_OK : al_hip_fail(e, "mul_mat_q4_0: fused launch");
+}
+
+template <int BPL>
+int launch_fused_t(const al_tensor * w, const al_tensor * x, const al_tensor * y, int N, int K, int T, hipStream_t st) {
+    return T == 1 ? launch_fused<BPL, 1>(w, x, y, N, K, T, st) : launch_fused<BPL, kFusedMaxT>(w, x, y, N, K, T, st);
 }
 
 // Per-device scratch for the quantized activations, grown on demand.
@@ -335,12 +387,12 @@ extern "C" int al_mul_mat_q4_0_f32(const al_tensor * w, const al_tensor * x, con
         (x->nb[1] & 15) || x->nb[1] < (uint64_t) K * 4 || y->nb[1] < (uint64_t) N * 4 || ((uintptr_t) y->data & 3))
         return al_fail(AL_ERR_INVALID, "mul_mat_q4_0: w rows must be contiguous blocks (nb1 = K/32*18, 4-byte aligned), x rows 16-byte aligned, rows not overlapping");
     hipStream_t st = (hipStream_t) stream;
-    if (fused_lds_bytes(K, T) <= kFusedLds) {
+    if (T <= kFusedMaxT) {
         switch (nb / 64) {
-            case 2: return launch_fused<2>(w, x, y, (int) N, (int) K, (int) T, st);
-            case 4: return launch_fused<4>(w, x, y, (int) N, (int) K, (int) T, st);
-            case 6: return launch_fused<6>(w, x, y, (int) N, (int) K, (int) T, st);
-            case 8: return launch_fused<8>(w, x, y, (int) N, (int) K, (int) T, st);
+            case 2: return launch_fused_t<2>(w, x, y, (int) N, (int) K, (int) T, st);
+            case 4: return launch_fused_t<4>(w, x, y, (int) N, (int) K, (int) T, st);
+            case 6: return launch_fused_t<6>(w, x, y, (int) N, (int) K, (int) T, st);
+            case 8: return launch_fused_t<8>(w, x, y, (int) N, (int) K, (int) T, st);
             default: return al_fail(AL_ERR_UNSUPPORTED, "mul_mat_q4_0: K %lld", (long long) K);
         }
     }

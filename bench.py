@@ -326,7 +326,8 @@ def main():
         print(json.dumps({"prefill": bench_prefill(lib, stream, a)}))
         return
     if a.only == "wo":
-        print(json.dumps({"wo": bench_wo(lib, stream, a)}))
+        print(json.dumps({"wo": [bench_wo(lib, stream, a, K=K, N=N, T=T, copies=c)
+                                 for K, N, T, c in [(4096, 2560, 1, 64), (4096, 2560, 8, 64), (8192, 5120, 1, 16)]]}))
         return
 
     dec = bench_decode(lib, stream, a)
