@@ -335,13 +335,15 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
                         vis_any[j] = vis_any[j] || vis;
                     }
             }
+            // lane-local maxima suffice to see that no score passes its row's
+            // reference by more than tau; the row maxima (a cross-lane
+            // reduction) are formed only on the rare path that moves it
             bool grow_any = false;
 #pragma unroll
             for (int rb = 0; rb < kPRB; ++rb) {
                 const float a = fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), s[rb][0][2]);
                 const float c = fmaxf(fmaxf(s[rb][0][3], s[rb][1][0]), s[rb][1][1]);
-                const float e = fmaxf(fmaxf(s[rb][1][2], s[rb][1][3]), fmaxf(a, c));
-                mt[rb] = colmax4(e);
+                mt[rb] = fmaxf(fmaxf(s[rb][1][2], s[rb][1][3]), fmaxf(a, c));
                 grow_any = grow_any || (mt[rb] > m_run[rb] + tau);
             }
             if (__any(grow_any)) break;
@@ -355,6 +357,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
         // tile `it` moves the reference max of some rows: scale, then finish it
 #pragma unroll
         for (int rb = 0; rb < kPRB; ++rb) {
+            mt[rb] = colmax4(mt[rb]);                                     // the row's max, same in its 4 lanes
             const bool grow = mt[rb] > m_run[rb] + tau;
             const float mn = grow ? mt[rb] : m_run[rb];
             const float alpha = grow ? __builtin_amdgcn_exp2f((m_run[rb] - mn) * cexp) : 1.0f;   // 0 from -inf
