@@ -8,9 +8,10 @@
 // Wave w takes row half w & 1 (32 rows: 2 MFMA row blocks, so each K/V
 // operand read from LDS feeds 2 MFMAs) and cell split w >> 1 (every 4th
 // 32-cell tile of the visible range). The two waves of a split sit on
-// different SIMDs and share the split's ring of two 16 KiB LDS stages: the
-// row-half-0 wave loads the tiles, publishes "tile landed" in an LDS flag,
-// and refills a stage once the row-half-1 wave has published "tile read".
+// different SIMDs and share the split's ring of two 16 KiB LDS stages: one of
+// them (row half 0 for splits 0 and 1, row half 1 for splits 2 and 3, so that
+// each SIMD hosts one) loads the tiles, publishes "tile landed" in an LDS
+// flag, and refills a stage once the other has published "tile read".
 // No workgroup barrier runs in the loop, so the splits drift apart and the
 // two waves on each SIMD (different splits) overlap each other's matrix and
 // vector work. A 512-token chunk of Qwen3-4B gives 32 row tiles x 8 kv heads
@@ -198,7 +199,10 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int nt = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
     const char * ring = &lds[cs * kNB * kStage];
     const uint32_t ring_addr = lds_addr(ring);
-    const bool loader = rh == 0;
+    // wave w runs on SIMD w % 4: splits 0 and 2 share SIMDs 0 and 1, splits 1
+    // and 3 SIMDs 2 and 3; the loading wave alternates between the row halves
+    // so that every SIMD hosts one loader and one reader
+    const bool loader = rh == ((cs >> 1) & 1);
 
     // The tile's query rows travel once, by LDS-DMA into the staging area
     // behind the rings, ahead of the first K/V tiles: wave w loads rows
