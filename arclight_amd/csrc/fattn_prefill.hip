@@ -122,15 +122,24 @@ __device__ __forceinline__ bool flag_wait(const int * f, int v) {
     return false;
 }
 
+// First cell of a split's it-th tile: the split walks its tiles starting at
+// tile rot (0 <= rot < nt) and wrapping around, so the workgroups of one kv
+// head (which share its K/V through one XCD's L2) are spread over the cell
+// range instead of all missing the same lines at the same time.
+__device__ __forceinline__ int tile_cell(const int cb0, const int it, const int rot, const int nt) {
+    const int j = it + rot;
+    return cb0 + (j < nt ? j : j - nt) * kStride;
+}
+
 // After the softmax of tile it, the loading wave refills the tile's stage
 // with tile it + 2 once the other wave has read it.
-__device__ __forceinline__ bool refill(const bool loader, const int it, const int nt, const int * done, const int4v kd,
-                                       const int4v vd, const uint32_t ring_addr, const int cb0, const uint32_t k_nb1,
-                                       const uint32_t v_nb1, const int g, const int n) {
+__device__ __forceinline__ bool refill(const bool loader, const int it, const int nt, const int rot, const int * done,
+                                       const int4v kd, const int4v vd, const uint32_t ring_addr, const int cb0,
+                                       const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n) {
     if (!loader || it + 2 >= nt) return true;
     const bool ok = flag_wait(done, it);
-    if (ok) issue_tile(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) (cb0 + (it + 2) * kStride), k_nb1,
-                       v_nb1, g, n);
+    if (ok) issue_tile(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) tile_cell(cb0, it + 2, rot, nt),
+                       k_nb1, v_nb1, g, n);
     return ok;
 }
 
@@ -194,9 +203,10 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int4v kd = raw_desc(kbase, (uint32_t) (p.n_kv - 1) * k_nb1 + 256);
     const int4v vd = raw_desc(vbase, (uint32_t) (p.n_kv - 1) * v_nb1 + 256);
 
-    // this split's tiles: cells cb0 + it * kStride, it < nt
+    // this split's tiles: cells cb0 + i * kStride, i < nt, in the order of tile_cell
     const int cb0 = cs * 32;
     const int nt = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
+    const int rot = nt > 0 ? (int) (((int64_t) rt * nt) / p.n_row_tiles) : 0;
     const char * ring = &lds[cs * kNB * kStage];
     const uint32_t ring_addr = lds_addr(ring);
     // wave w runs on SIMD w % 4: splits 0 and 2 share SIMDs 0 and 1, splits 1
@@ -222,8 +232,9 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
                   lds_addr(qst) + (uint32_t) ((8 * wave + 2 * i) * 512));
         }
     }
-    if (loader && nt > 0) issue_tile(kd, vd, ring_addr, (uint32_t) cb0, k_nb1, v_nb1, g, n);
-    if (loader && nt > 1) issue_tile(kd, vd, ring_addr + kStage, (uint32_t) (cb0 + kStride), k_nb1, v_nb1, g, n);
+    if (loader && nt > 0) issue_tile(kd, vd, ring_addr, (uint32_t) tile_cell(cb0, 0, rot, nt), k_nb1, v_nb1, g, n);
+    if (loader && nt > 1)
+        issue_tile(kd, vd, ring_addr + kStage, (uint32_t) tile_cell(cb0, 1, rot, nt), k_nb1, v_nb1, g, n);
     wait_later<2, 16>(loader ? min(nt, 2) : 0);                      // own query rows landed
     __syncthreads();                                                   // everyone's
 
@@ -306,7 +317,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));                 // lgkmcnt(0): the stage is read
             mem_barrier();
             if (!loader) flag_set(landed + kCS, it);                       // done[cs]
-            const int cb = cb0 + it * kStride;
+            const int cb = tile_cell(cb0, it, rot, nt);
 
             // S^T = K Q^T: cells 4g+i (mb 0) and 16+4g+i (mb 1) of row n
 #pragma unroll
@@ -352,7 +363,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             }
             if (__any(grow_any)) break;
             accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-            if (!refill(loader, it, nt, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
+            if (!refill(loader, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
                 ok = false;
                 break;
             }
@@ -371,7 +382,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             m_run[rb] = mn;
         }
         accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-        ok = refill(loader, it, nt, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
+        ok = refill(loader, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
         ++it;
     }
     if (!ok && lane == 0) atomicOr(p.err + 2, 1);                      // reported by al_device_errors
