@@ -196,15 +196,18 @@ int decode_wgs_per_cu() {
 }
 // Decode kernel shape: wavefronts per workgroup (AL_DECODE_WAVES) and LDS
 // stage buffers per wave (AL_DECODE_STAGES); combinations without a kernel
-// fall back to 2 x 3, the fastest measured at 32K context (fewer, deeper
-// streams per CU beat more of them).
-int decode_waves() {
-    static int v = env_int("AL_DECODE_WAVES", 2);
-    return v;
+// fall back to 2 x 3. Unset: 2 x 3 for up to 4 query rows per kv head
+// (decode; fewer, deeper streams per CU beat more of them), 8 x 2 for more
+// (speculative verify, whose final merge of 16-row records is bound by the
+// lanes the last workgroup brings to it: 8192-cell context, 16 rows, 24.5 us
+// per call with 2 x 3, 20.4 us with 8 x 2).
+int decode_waves(int rows) {
+    static int v = env_int("AL_DECODE_WAVES", 0);
+    return v > 0 ? v : (rows <= 4 ? 2 : 8);
 }
-int decode_stages() {
-    static int v = env_int("AL_DECODE_STAGES", 3);
-    return v;
+int decode_stages(int rows) {
+    static int v = env_int("AL_DECODE_STAGES", 0);
+    return v > 0 ? v : (rows <= 4 ? 3 : 2);
 }
 // AL_DECODE_INTERLEAVE=0: each split takes a contiguous cell range.
 bool decode_interleave() {
@@ -325,7 +328,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
 
     // Up to 16 rows per kv head: the decode kernel, when its LDS rings fit
     // and a head's K/V view is addressable with 32-bit offsets.
-    int dwaves = decode_waves(), stages = decode_stages();
+    int dwaves = decode_waves(p.R), stages = decode_stages(p.R);
     if (!fattn_decode_config_ok(dwaves, stages)) {
         dwaves = 2;
         stages = 3;
