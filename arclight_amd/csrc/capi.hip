@@ -196,18 +196,19 @@ int decode_wgs_per_cu() {
 }
 // Decode kernel shape: wavefronts per workgroup (AL_DECODE_WAVES) and LDS
 // stage buffers per wave (AL_DECODE_STAGES); combinations without a kernel
-// fall back to 2 x 3. Unset: 2 x 3 for up to 4 query rows per kv head
-// (decode; fewer, deeper streams per CU beat more of them), 8 x 2 for more
-// (speculative verify, whose final merge of 16-row records is bound by the
-// lanes the last workgroup brings to it: 8192-cell context, 16 rows, 24.5 us
-// per call with 2 x 3, 20.4 us with 8 x 2).
+// fall back to 2 x 3. Unset: 2 x 3 for up to 8 query rows per kv head
+// (decode and 2-draft verify; fewer, deeper streams per CU beat more of
+// them), 8 x 2 for more (verify of 4 or more drafts, whose final merge of
+// 16- or 32-row records is bound by the lanes the last workgroup brings to
+// it: 16 rows at 4096 / 16384 / 32768 cells take 21.8 / 28.9 / 37.7 us with
+// 2 x 3 and 15.0 / 25.7 / 37.5 us with 8 x 2).
 int decode_waves(int rows) {
     static int v = env_int("AL_DECODE_WAVES", 0);
-    return v > 0 ? v : (rows <= 4 ? 2 : 8);
+    return v > 0 ? v : (rows <= 8 ? 2 : 8);
 }
 int decode_stages(int rows) {
     static int v = env_int("AL_DECODE_STAGES", 0);
-    return v > 0 ? v : (rows <= 4 ? 3 : 2);
+    return v > 0 ? v : (rows <= 8 ? 3 : 2);
 }
 // AL_DECODE_INTERLEAVE=0: each split takes a contiguous cell range.
 bool decode_interleave() {
@@ -326,25 +327,35 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         return AL_OK;
     }
 
-    // Up to 16 rows per kv head: the decode kernel, when its LDS rings fit
-    // and a head's K/V view is addressable with 32-bit offsets.
+    // Up to 16 rows per kv head (32 with implicit masks): the decode kernel,
+    // when its LDS rings fit and a head's K/V view is addressable with 32-bit
+    // offsets.
     int dwaves = decode_waves(p.R), stages = decode_stages(p.R);
     if (!fattn_decode_config_ok(dwaves, stages)) {
         dwaves = 2;
         stages = 3;
     }
+    // 17..32 rows (two row blocks) exist as 8 x 2 with implicit masks only
+    const bool two_blocks = p.R > 16;
+    if (two_blocks) {
+        dwaves = 8;
+        stages = 2;
+    }
     const size_t decode_lds = fattn_decode_lds_bytes(dwaves, stages, m.data != nullptr);
     const bool mask_ok = !m.data || (p.m_slice_bytes < INT32_MAX && aligned16(m.data) && m.nb[1] % 16 == 0 &&
                                      m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
     const int64_t decode_units = Hkv * B;
-    if (p.R <= 16 && prefer_decode() && (size_t) lds_per_block >= decode_lds && mask_ok && q_slice < INT32_MAX &&
+    const size_t decode_q_lds = two_blocks ? 16384 : 8192;                 // the query rows, f32
+    if ((p.R <= 16 || (p.R <= 32 && !m.data)) && prefer_decode() && (size_t) lds_per_block >= decode_lds + decode_q_lds &&
+        mask_ok &&
+        q_slice < INT32_MAX &&
         decode_units * sizeof(unsigned) <= kFattnCounterBytes &&
         (uint64_t) (n_kv + 16) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
         (uint64_t) (n_kv + 16) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX) {
         pl.kernel = kDecode;
         pl.waves = dwaves;
         pl.stages = stages;
-        pl.rows_per_tile = 16;
+        pl.rows_per_tile = two_blocks ? 32 : 16;
         p.n_row_tiles = 1;
         int64_t extent = p.kv_hi;
         if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
@@ -363,7 +374,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.interleave = decode_interleave() ? 1 : 0;
         if (p.n_split > 1) {
             pl.counters_bytes = kFattnCounterBytes;
-            pl.part_bytes = (size_t) decode_units * p.n_split * 16 * kFattnRecordStride * sizeof(float);
+            pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
         }
         *out = pl;
         return AL_OK;

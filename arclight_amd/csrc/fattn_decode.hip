@@ -5,7 +5,8 @@
 //
 // Work decomposition. A workgroup owns one kv head of one cell range (a
 // split) of one stream and keeps up to 16 query rows of the head's group
-// (row r -> token r / G, head kvh*G + r % G). Its WS wavefronts take the
+// (row r -> token r / G, head kvh*G + r % G), or up to 32 as two MFMA row
+// blocks sharing every K/V operand read (speculative verify, implicit masks). Its WS wavefronts take the
 // range's 16-cell stages in turn (wave ws: stages ws, ws + WS, ...), each
 // with a private ring of NB LDS stage buffers, so the waves never wait for
 // each other until the end. The 1-D grid runs split fastest.
@@ -45,15 +46,16 @@ using namespace fattn;
 
 constexpr int kSC = 16;                                   // cells per stage
 
-template <int WS, int NB, bool HAS_MASK>
+template <int WS, int NB, bool HAS_MASK, int RB>
 __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p) {
     static_assert(WS == 2 || WS == 4 || WS == 8, "the wave merge is a binary tree");
+    static_assert(RB == 1 || (RB == 2 && !HAS_MASK), "32 rows with implicit masks only");
     constexpr int PER = 8 + (HAS_MASK ? 1 : 0);           // DMA loads per stage
     constexpr int STAGE = 8192 + (HAS_MASK ? 1024 : 0);   // K rows, V rows, mask rows
-    constexpr int REC = 16 * kRowStride;                  // floats of one 16-row state record
+    constexpr int REC = 16 * RB * kRowStride;             // floats of one state record (16 RB rows)
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
-    __shared__ __attribute__((aligned(1024))) char qlds[16 * 512];  // the 16 query rows, f32
+    __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
     __shared__ int s_last;
 
     const int lane = threadIdx.x & 63;
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const int kvh = id % p.Hkv;
     const int b = id / p.Hkv;
     const int unit = b * p.Hkv + kvh;
-    const int rows_here = min(16, p.R);
+    const int rows_here = min(16 * RB, p.R);
     const int t_last = (rows_here - 1) / p.G;
 
     int hi = p.kv_hi;
@@ -99,11 +101,16 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     for (int i = 0; i < 4; ++i) dj[i] = (uint32_t) (((lane & 15) ^ (4 * i + dcell)) * 16);
     const uint32_t ring = lds_addr(&lds[ws][0][0]);
 
-    // this lane's query row: column n of the single row block
-    const int r = n;
-    const bool rvalid = r < rows_here;
-    const int tok = rvalid ? r / p.G : 0;
-    const int head = kvh * p.G + (rvalid ? r % p.G : 0);
+    // this lane's query rows: column n of each row block (row 16 rb + n)
+    bool rvalid[RB];
+    int tok[RB], head[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int r = 16 * rb + n;
+        rvalid[rb] = r < rows_here;
+        tok[rb] = rvalid[rb] ? r / p.G : 0;
+        head[rb] = kvh * p.G + (rvalid[rb] ? r % p.G : 0);
+    }
 
     // Mask rows (f16, cells along a row) also travel by DMA, one 1 KiB block
     // per stage: lane l < 32 loads cells 8(l & 1)..+7 of row l >> 1 to LDS
@@ -156,31 +163,42 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     __syncthreads();
 
     // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
-    half8 qf[4];
-    {
-        const char * qrow = qlds + n * 512;
+    half8 qf[RB][4];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const char * qrow = qlds + (16 * rb + n) * 512;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb) {
-            const int j = 2 * (4 * kb + g);                               // granules j, j + 1 of row n
+            const int j = 2 * (4 * kb + g);                               // granules j, j + 1 of the row
             const float4 qa = *(const float4 *) (qrow + ((j ^ (2 * n)) & 31) * 16);
             const float4 qb = *(const float4 *) (qrow + (((j + 1) ^ (2 * n)) & 31) * 16);
-            qf[kb] = rvalid ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+            qf[rb][kb] = rvalid[rb] ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
 
-    float slope = 1.0f;
-    if (p.max_bias > 0.0f) {                                           // arm.cpp:2294
-        const uint32_t hq = (uint32_t) head;
-        slope = hq < p.n_head_log2 ? powf(p.m0, (float) (hq + 1)) : powf(p.m1, (float) (2 * (hq - p.n_head_log2) + 1));
+    float slope[RB];
+    int lim[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        slope[rb] = 1.0f;
+        if (p.max_bias > 0.0f) {                                       // arm.cpp:2294
+            const uint32_t hq = (uint32_t) head[rb];
+            slope[rb] = hq < p.n_head_log2 ? powf(p.m0, (float) (hq + 1))
+                                           : powf(p.m1, (float) (2 * (hq - p.n_head_log2) + 1));
+        }
+        lim[rb] = row_limit(p, hi, rvalid[rb], tok[rb]);
     }
-    const int lim = row_limit(p, hi, rvalid, tok);
     const int lim_min = row_limit(p, hi, true, 0);
 
-    floatx4 o[8];
+    floatx4 o[RB][8];
+    float m_run[RB], l_run[RB];
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) o[mb] = floatx4{0, 0, 0, 0};
-    float m_run = -AL_INF;
-    float l_run = 0.0f;
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb) o[rb][mb] = floatx4{0, 0, 0, 0};
+        m_run[rb] = -AL_INF;
+        l_run[rb] = 0.0f;
+    }
 
     // LDS read offsets of this lane within a stage
     const int kread = n * 256;                                          // K row of cell n
@@ -208,52 +226,55 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             uint2 mk = {0, 0};
             if constexpr (HAS_MASK) mk = *(const uint2 *) (st + 8192 + 32 * n + 8 * g);
 
-            // S^T: cells 4g+i of row n
-            floatx4 sc = {0, 0, 0, 0};
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) sc = mfma_16x16x32(as_half8(kf[kb]), qf[kb], sc);
-            sc *= p.scale;
-            if (p.softcap != 0.0f) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i) sc[i] = p.softcap * tanhf(sc[i]);
-            }
             const bool full = !HAS_MASK && cs + kSC - 1 <= lim_min;
-            bool vis_any[4] = {true, true, true, true};
-            if (!full) {
+            bool vis_any[4] = {!!full, !!full, !!full, !!full};
+            half4 pf[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                // S^T: cells 4g+i of row 16 rb + n
+                floatx4 sc = {0, 0, 0, 0};
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) sc = mfma_16x16x32(as_half8(kf[kb]), qf[rb][kb], sc);
+                sc *= p.scale;
+                if (p.softcap != 0.0f) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) sc[i] = p.softcap * tanhf(sc[i]);
+                }
+                if (!full) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        bool vis = cs + 4 * g + i <= lim[rb];
+                        float x = sc[i];
+                        if constexpr (HAS_MASK) {
+                            const uint32_t w = i < 2 ? mk.x : mk.y;
+                            const float mv = slope[rb] * f16_bits_to_float((uint16_t) (w >> (16 * (i & 1))));
+                            vis = vis && (mv != -AL_INF);
+                            x += mv;
+                        }
+                        sc[i] = vis ? x : -AL_INF;
+                        vis_any[i] = vis_any[i] || vis;
+                    }
+                }
+                const float mt = colmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
+                if (__any(mt > m_run[rb] + kTau)) {
+                    const bool grow = mt > m_run[rb] + kTau;
+                    const float mn = grow ? mt : m_run[rb];
+                    const float alpha = grow ? exp_fast(m_run[rb] - mn) : 1.0f;
+                    l_run[rb] *= alpha;
+#pragma unroll
+                    for (int mb = 0; mb < 8; ++mb) o[rb][mb] *= alpha;
+                    m_run[rb] = mn;
+                }
+                const float mu = (m_run[rb] == -AL_INF) ? 0.0f : m_run[rb];
+                float ps = 0.0f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    bool vis = cs + 4 * g + i <= lim;
-                    float x = sc[i];
-                    if constexpr (HAS_MASK) {
-                        const uint32_t w = i < 2 ? mk.x : mk.y;
-                        const float mv = slope * f16_bits_to_float((uint16_t) (w >> (16 * (i & 1))));
-                        vis = vis && (mv != -AL_INF);
-                        x += mv;
-                    }
-                    sc[i] = vis ? x : -AL_INF;
-                    vis_any[i] = vis;
+                    const float pr = exp_fast(sc[i] - mu);
+                    ps += pr;
+                    pf[rb][i] = (_Float16) pr;
                 }
+                l_run[rb] += ps;
             }
-            const float mt = colmax4(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-            if (__any(mt > m_run + kTau)) {
-                const bool grow = mt > m_run + kTau;
-                const float mn = grow ? mt : m_run;
-                const float alpha = grow ? exp_fast(m_run - mn) : 1.0f;
-                l_run *= alpha;
-#pragma unroll
-                for (int mb = 0; mb < 8; ++mb) o[mb] *= alpha;
-                m_run = mn;
-            }
-            const float mu = (m_run == -AL_INF) ? 0.0f : m_run;
-            half4 pf;
-            float ps = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float pr = exp_fast(sc[i] - mu);
-                ps += pr;
-                pf[i] = (_Float16) pr;
-            }
-            l_run += ps;
             if (!full) {
                 // cells masked for every row contribute exact zeros, whatever their V holds
 #pragma unroll
@@ -266,10 +287,13 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                 }
             }
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb) o[mb] = mfma_16x16x16(vt[mb], pf, o[mb]);
+            for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) o[rb][mb] = mfma_16x16x16(vt[mb], pf[rb], o[rb][mb]);
         }
     }
-    l_run = colsum4(l_run);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) l_run[rb] = colsum4(l_run[rb]);
 
     // merge the WS waves through LDS records [slot][row][132] (the rings are
     // free once every wave is past its loop)
@@ -279,40 +303,50 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         for (int span = WS / 2; span >= 1; span /= 2) {
             __syncthreads();
             if (ws >= span && ws < 2 * span) {
-                float * rec = recs + (ws - span) * REC + n * kRowStride;
 #pragma unroll
-                for (int mb = 0; mb < 8; ++mb) *(float4 *) (rec + 16 * mb + 4 * g) = float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]};
-                if (g == 0) *(float2 *) (rec + 128) = float2{m_run, l_run};
+                for (int rb = 0; rb < RB; ++rb) {
+                    float * rec = recs + (ws - span) * REC + (16 * rb + n) * kRowStride;
+#pragma unroll
+                    for (int mb = 0; mb < 8; ++mb)
+                        *(float4 *) (rec + 16 * mb + 4 * g) = float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]};
+                    if (g == 0) *(float2 *) (rec + 128) = float2{m_run[rb], l_run[rb]};
+                }
             }
             __syncthreads();
             if (ws < span) {
-                const float * rec = recs + ws * REC + n * kRowStride;
-                const float2 ml = *(const float2 *) (rec + 128);
-                const float mn = fmaxf(m_run, ml.x);
-                const float mu = (mn == -AL_INF) ? 0.0f : mn;
-                const float wa = exp_fast(m_run - mu);
-                const float wb = exp_fast(ml.x - mu);
 #pragma unroll
-                for (int mb = 0; mb < 8; ++mb) {
-                    const float4 x = *(const float4 *) (rec + 16 * mb + 4 * g);
-                    o[mb][0] = o[mb][0] * wa + x.x * wb;
-                    o[mb][1] = o[mb][1] * wa + x.y * wb;
-                    o[mb][2] = o[mb][2] * wa + x.z * wb;
-                    o[mb][3] = o[mb][3] * wa + x.w * wb;
+                for (int rb = 0; rb < RB; ++rb) {
+                    const float * rec = recs + ws * REC + (16 * rb + n) * kRowStride;
+                    const float2 ml = *(const float2 *) (rec + 128);
+                    const float mn = fmaxf(m_run[rb], ml.x);
+                    const float mu = (mn == -AL_INF) ? 0.0f : mn;
+                    const float wa = exp_fast(m_run[rb] - mu);
+                    const float wb = exp_fast(ml.x - mu);
+#pragma unroll
+                    for (int mb = 0; mb < 8; ++mb) {
+                        const float4 x = *(const float4 *) (rec + 16 * mb + 4 * g);
+                        o[rb][mb][0] = o[rb][mb][0] * wa + x.x * wb;
+                        o[rb][mb][1] = o[rb][mb][1] * wa + x.y * wb;
+                        o[rb][mb][2] = o[rb][mb][2] * wa + x.z * wb;
+                        o[rb][mb][3] = o[rb][mb][3] * wa + x.w * wb;
+                    }
+                    l_run[rb] = l_run[rb] * wa + ml.y * wb;
+                    m_run[rb] = mn;
                 }
-                l_run = l_run * wa + ml.y * wb;
-                m_run = mn;
             }
         }
     }
 
     if (p.n_split == 1) {
-        if (ws == 0 && rvalid) {
-            float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok) * p.Hq + head) * p.dst_nb1);
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb)
-                *(float4 *) (out + 16 * mb + 4 * g) =
-                    finalize4(float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]}, m_run, l_run, p.sinks, head);
+        for (int rb = 0; rb < RB; ++rb) {
+            if (ws == 0 && rvalid[rb]) {
+                float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok[rb]) * p.Hq + head[rb]) * p.dst_nb1);
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb)
+                    *(float4 *) (out + 16 * mb + 4 * g) = finalize4(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]},
+                                                                    m_run[rb], l_run[rb], p.sinks, head[rb]);
+            }
         }
         return;
     }
@@ -320,12 +354,16 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     // publish this split's record: [unit][split][row][132]
     constexpr uint32_t RS = REC * 4;                                   // bytes of one split's record
     const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * REC, RS * (uint32_t) p.n_split);
-    if (ws == 0 && rvalid) {
-        const uint32_t row = (uint32_t) split * RS + (uint32_t) (r * kRowStride * 4);
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb)
-            buf_store16_dev(float4{o[mb][0], o[mb][1], o[mb][2], o[mb][3]}, pr, row + (16 * mb + 4 * g) * 4);
-        if (g == 0) buf_store8_dev(float2{m_run, l_run}, pr, row + 128 * 4);
+    for (int rb = 0; rb < RB; ++rb) {
+        if (ws == 0 && rvalid[rb]) {
+            const uint32_t row = (uint32_t) split * RS + (uint32_t) ((16 * rb + n) * kRowStride * 4);
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb)
+                buf_store16_dev(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]}, pr,
+                                row + (16 * mb + 4 * g) * 4);
+            if (g == 0) buf_store8_dev(float2{m_run[rb], l_run[rb]}, pr, row + 128 * 4);
+        }
     }
     complete_wave_memops();
     __syncthreads();
@@ -338,16 +376,17 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 
     // Last workgroup: two adjacent lanes per (row, 4 dims), each taking 16
     // of the at most 32 splits, then combining with its partner (split half
-    // 0 first, on both lanes). A thread takes two such items per round with
-    // all 64 of their loads in flight, so a decode merge (4 rows = 256
-    // items) is one round trip.
+    // 0 first, on both lanes). A thread takes two such items per round (one
+    // with two row blocks, for registers) with all of their loads in flight,
+    // so a decode merge (4 rows = 256 items) is one round trip.
     constexpr int kHalf = kMaxSplit / 2;
+    constexpr int kItems = RB == 1 ? 2 : 1;                            // items per thread and round (registers)
     const int n_items = rows_here * 64;
-    for (int base = 0; base < n_items; base += 2 * WS * 64) {
-        float2 ml[2][kHalf];
-        float4 ov[2][kHalf];
+    for (int base = 0; base < n_items; base += kItems * WS * 64) {
+        float2 ml[kItems][kHalf];
+        float4 ov[kItems][kHalf];
 #pragma unroll
-        for (int it2 = 0; it2 < 2; ++it2) {
+        for (int it2 = 0; it2 < kItems; ++it2) {
             const int idx = base + it2 * WS * 64 + threadIdx.x;
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
@@ -366,7 +405,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             }
         }
 #pragma unroll
-        for (int it2 = 0; it2 < 2; ++it2) {
+        for (int it2 = 0; it2 < kItems; ++it2) {
             const int idx = base + it2 * WS * 64 + threadIdx.x;
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
@@ -401,8 +440,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 template <int WS, int NB>
 hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
     const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
-    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true>), grid, dim3(WS * 64), 0, stream, p);
-    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false>), grid, dim3(WS * 64), 0, stream, p);
+    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true, 1>), grid, dim3(WS * 64), 0, stream, p);
+    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1>), grid, dim3(WS * 64), 0, stream, p);
     return hipGetLastError();
 }
 
@@ -420,6 +459,13 @@ size_t fattn_decode_lds_bytes(int waves, int stages, bool mask) {
 }
 
 hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream) {
+    if (p.R > 16) {
+        // 17..32 rows: two row blocks, implicit masks, 8 waves x 2 stages
+        if (p.R > 32 || p.mask || waves != 8 || stages != 2) return hipErrorInvalidValue;
+        const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
+        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2>), grid, dim3(8 * 64), 0, stream, p);
+        return hipGetLastError();
+    }
     switch (waves * 10 + stages) {
         case 23: return launch_cfg<2, 3>(p, stream);
         case 24: return launch_cfg<2, 4>(p, stream);
