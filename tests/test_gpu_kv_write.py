@@ -32,7 +32,8 @@ def test_f32_to_f16_bits_match_numpy(gpu):
     call("al_util_f32_to_f16", dh.ptr, dx.ptr, x.size, None)
     got = np.empty(x.size, dtype=np.uint16)
     dh.download(got)
-    want = x.astype(np.float16).view(np.uint16)
+    with np.errstate(over="ignore"):                                  # values past f16 range round to inf
+        want = x.astype(np.float16).view(np.uint16)
     nan = np.isnan(x)
     assert np.array_equal(got[~nan], want[~nan])
     assert np.isnan(got[nan].view(np.float16)).all()
