@@ -66,6 +66,7 @@ class AlFattnArgs(ctypes.Structure):
         ("stream", ctypes.c_void_p),
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_uint64),
+        ("dyn_len", ctypes.c_void_p),
     ]
 
 

@@ -303,6 +303,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     p.n_kv = (int32_t) n_kv;
     p.kv_hi = (int32_t) ((a->kv_len <= 0 || a->kv_len > n_kv) ? n_kv : a->kv_len);
     p.causal_pos0 = a->causal_pos0 < 0 ? -1 : a->causal_pos0;
+    p.dyn = a->dyn_len;
+    if (p.dyn && m.data) return al_fail(AL_ERR_UNSUPPORTED, "fattn: dyn_len needs implicit masking (no mask tensor)");
     p.softcap = a->logit_softcap;
     p.scale = a->scale;
     if (p.softcap != 0.0f) p.scale /= p.softcap;                        // arm.cpp:2267-2269
@@ -315,7 +317,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     // workgroup per 64-row tile, when that alone fills the device.
     const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
     // (it keeps the running max on scores as computed: needs scale > 0 unless softcapped)
-    if (!m.data && p.R > 32 && prefill_tiles * Hkv * B >= n_cu && lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
+    if (!m.data && !p.dyn && p.R > 32 && prefill_tiles * Hkv * B >= n_cu &&
+        lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
         q_slice < INT32_MAX &&
         (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill()) {
         pl.kernel = kPrefill;
@@ -357,8 +360,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         pl.stages = stages;
         pl.rows_per_tile = two_blocks ? 32 : 16;
         p.n_row_tiles = 1;
-        int64_t extent = p.kv_hi;
-        if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
+        int64_t extent = p.kv_hi;                                       // with dyn_len: the bound
+        if (p.causal_pos0 >= 0 && !p.dyn) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
         extent = std::max<int64_t>(extent, 0);
         const int64_t nst = std::max<int64_t>(1, (extent + 15) / 16);   // 16-cell stages
         // workgroups resident per CU by LDS (160 KiB per CU on gfx950)
@@ -379,6 +382,9 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         *out = pl;
         return AL_OK;
     }
+
+    if (p.dyn)
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn: dyn_len needs the decode kernel (up to 32 query rows per kv head)");
 
     // split-KV sizing
     pl.rows_per_tile = fattn_splitkv_rows_per_tile(std::min(p.R, 64));

@@ -72,8 +72,14 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const int rows_here = min(16 * RB, p.R);
     const int t_last = (rows_here - 1) / p.G;
 
+    // lengths: fixed at launch, or read now (a graph replayed per decode step)
     int hi = p.kv_hi;
-    if (p.causal_pos0 >= 0) hi = (int) min((int64_t) hi, p.causal_pos0 + t_last + 1);
+    int64_t cpos0 = p.causal_pos0;
+    if (p.dyn) {
+        hi = min(max(p.dyn[0], 0), p.kv_hi);
+        if (cpos0 >= 0) cpos0 = max(p.dyn[1], 0);
+    }
+    if (cpos0 >= 0) hi = (int) min((int64_t) hi, cpos0 + t_last + 1);
     // Stages of this workgroup: with interleave, global 16-cell stages
     // split, split + n_split, ... of [0, hi) (all splits of a head sweep the
     // cache together); else the contiguous range [c_begin, c_end). Wave ws
@@ -186,9 +192,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             slope[rb] = hq < p.n_head_log2 ? powf(p.m0, (float) (hq + 1))
                                            : powf(p.m1, (float) (2 * (hq - p.n_head_log2) + 1));
         }
-        lim[rb] = row_limit(p, hi, rvalid[rb], tok[rb]);
+        lim[rb] = row_limit(cpos0, hi, rvalid[rb], tok[rb]);
     }
-    const int lim_min = row_limit(p, hi, true, 0);
+    const int lim_min = row_limit(cpos0, hi, true, 0);
 
     floatx4 o[RB][8];
     float m_run[RB], l_run[RB];

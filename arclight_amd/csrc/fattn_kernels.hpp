@@ -34,6 +34,7 @@ struct FattnParams {
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
     int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
+    const int32_t * dyn;            // decode kernel: device {kv_len, causal_pos0} read at run time, or null
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).

@@ -84,11 +84,14 @@ __device__ __forceinline__ void load_tile(Tile<RB> & t, const FattnParams & p, c
 }
 
 // Last visible cell of a query row under the length / causal rule.
-__device__ __forceinline__ int row_limit(const FattnParams & p, const int hi, const bool valid, const int tok) {
+__device__ __forceinline__ int row_limit(const int64_t causal_pos0, const int hi, const bool valid, const int tok) {
     if (!valid) return -1;
     int64_t lim = hi - 1;
-    if (p.causal_pos0 >= 0) lim = min(lim, p.causal_pos0 + tok);
+    if (causal_pos0 >= 0) lim = min(lim, causal_pos0 + tok);
     return (int) lim;
+}
+__device__ __forceinline__ int row_limit(const FattnParams & p, const int hi, const bool valid, const int tok) {
+    return row_limit(p.causal_pos0, hi, valid, tok);
 }
 
 // One merge record (O[128], m, l per query row) in LDS.

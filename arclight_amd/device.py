@@ -140,6 +140,30 @@ class Event:
             self.handle = None
 
 
+class Graph:
+    """A HIP graph of the work enqueue() puts on `stream` (captured, not
+    run): replayed by launch(). Everything the captured calls touch must
+    exist before capture (device buffers, the library's workspaces, which a
+    first eager call allocates)."""
+
+    def __init__(self, stream, enqueue):
+        call("al_util_graph_begin", stream.handle)
+        ge = ctypes.c_void_p()
+        try:
+            enqueue()
+        finally:
+            call("al_util_graph_end", stream.handle, ctypes.byref(ge))
+        self.handle = ge.value
+
+    def launch(self, stream):
+        call("al_util_graph_launch", self.handle, stream.handle)
+
+    def destroy(self):
+        if self.handle:
+            call("al_util_graph_destroy", self.handle)
+            self.handle = None
+
+
 def synchronize():
     call("al_util_device_synchronize")
 

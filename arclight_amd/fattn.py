@@ -22,7 +22,7 @@ from .device import DeviceTensor
 
 
 def fattn_args(q, k, v, mask=None, sinks=None, dst=None, *, scale, max_bias=0.0, logit_softcap=0.0,
-               prec=abi.AL_PREC_F32, kv_len=0, causal_pos0=-1, stream=None, workspace=None):
+               prec=abi.AL_PREC_F32, kv_len=0, causal_pos0=-1, stream=None, workspace=None, dyn_len=None):
     a = abi.AlFattnArgs()
     a.q = q.desc()
     a.k = k.desc()
@@ -40,17 +40,24 @@ def fattn_args(q, k, v, mask=None, sinks=None, dst=None, *, scale, max_bias=0.0,
     if workspace is not None:
         a.workspace = workspace.ptr
         a.workspace_bytes = workspace.nbytes
+    if dyn_len is not None:
+        a.dyn_len = dyn_len.ptr
     return a
 
 
 def flash_attn_ext(q, k, v, mask=None, sinks=None, *, scale, max_bias=0.0, logit_softcap=0.0,
-                   prec=abi.AL_PREC_F32, dst=None, kv_len=0, causal_pos0=-1, stream=None, workspace=None):
-    """Enqueues the op on `stream` and returns dst (allocated when None)."""
+                   prec=abi.AL_PREC_F32, dst=None, kv_len=0, causal_pos0=-1, stream=None, workspace=None,
+                   dyn_len=None):
+    """Enqueues the op on `stream` and returns dst (allocated when None).
+    dyn_len: an int32 (2,) DeviceTensor {kv_len, causal_pos0} read when the
+    kernel runs (for graphs replayed per decode step); kv_len is then the
+    bound and causal_pos0 >= 0 selects causal masking."""
     if dst is None:
         B, T, Hq = q.shape[0], q.shape[1], q.shape[2]
         dst = DeviceTensor.empty((B, T, Hq, v.shape[3]), np.float32, axes=abi.DST_AXES)
     a = fattn_args(q, k, v, mask, sinks, dst, scale=scale, max_bias=max_bias, logit_softcap=logit_softcap,
-                   prec=prec, kv_len=kv_len, causal_pos0=causal_pos0, stream=stream, workspace=workspace)
+                   prec=prec, kv_len=kv_len, causal_pos0=causal_pos0, stream=stream, workspace=workspace,
+                   dyn_len=dyn_len)
     call("al_fattn_f16", ctypes.byref(a))
     return dst
 

@@ -96,6 +96,18 @@ typedef struct al_tensor {
  * 256 KiB hold arrival counters that every call leaves at zero again, the
  * rest holds per-call merge records. Calls that share one workspace must be
  * ordered on one stream.
+ *
+ * dyn_len: for a call captured once into a HIP graph and replayed for every
+ * decode step (the GPU form of the reference's graph reuse while n_kv stays
+ * within the built graph's, nnml/src/context.cpp:177-205), a device pointer
+ * to two int32 {kv_len, causal_pos0} that the kernel reads when it runs.
+ * The host kv_len is then the largest length the replays will use (it sizes
+ * the launch) and causal_pos0 >= 0 only selects causal masking; the device
+ * values must satisfy 0 < kv_len <= that bound and, when causal,
+ * causal_pos0 + T <= kv_len. Needs implicit masking (no mask tensor) and up
+ * to 32 query rows per kv head (the decode kernel); else AL_ERR_UNSUPPORTED.
+ * Capture only after one eager call with the same shapes (workspaces are
+ * allocated on first use).
  */
 typedef struct al_fattn_args {
     al_tensor q;
@@ -113,6 +125,7 @@ typedef struct al_fattn_args {
     void *    stream;         /* hipStream_t; NULL = default stream */
     void *    workspace;
     uint64_t  workspace_bytes;
+    const int32_t * dyn_len;  /* optional device {kv_len, causal_pos0}, see below */
 } al_fattn_args;
 
 /*
