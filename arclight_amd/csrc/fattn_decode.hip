@@ -31,6 +31,11 @@
 // P^T comes from S^T in place: both keep cell 4g+i, row n in lane 16g+n.
 // O^T lane 16g+n holds dims 16mb + 4g + i of row n (mb = 0..7).
 //
+// Lengths. kv_len and causal_pos0 come with the launch, or (p.dyn, for a
+// graph captured once and replayed every decode step) from device memory
+// when the kernel runs, bounded by the launch's kv_len; splits whose stages
+// lie past the run-time length publish empty records.
+//
 // Merge. The WS waves merge their online-softmax states through LDS. With
 // one split the workgroup then writes dst; otherwise it publishes one
 // record per row with device-coherent stores, bumps the arrival counter of

@@ -148,3 +148,21 @@ def test_dyn_len_rejected_off_the_decode_path(gpu):
     with pytest.raises(_lib.ArclightError) as e:
         fattn.flash_attn_ext(q1, dk, dv, m, scale=0.1, dyn_len=dyn)
     assert e.value.status == abi.AL_ERR_UNSUPPORTED
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_dyn_len_matches_host_lengths(gpu, T):
+    """The run-time {kv_len, causal_pos0} give the same result as the same
+    lengths passed on the host, for decode and for 4- and 8-draft verify
+    (one and two row blocks), with the launch sized for a larger bound."""
+    from arclight_amd import device, fattn
+    _case(f"dyn_len T={T}")
+    n_kv, C = 1024, 700
+    q, k, v = O.make_inputs(40 + T, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    dyn = device.DeviceTensor.from_numpy(np.array([C + T, C], np.int32))
+    got = fattn.flash_attn_ext(dq, dk, dv, scale=0.08, kv_len=n_kv, causal_pos0=0, dyn_len=dyn)
+    device.synchronize()
+    fattn.device_errors()
+    ref = O.attention(q, k, v, O.causal_mask(T, n_kv, C, kv_len=C + T), scale=0.08)
+    assert_parity(got.numpy(np.float32), ref, what=f"dyn_len T={T}")
