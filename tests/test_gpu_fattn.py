@@ -280,3 +280,18 @@ def test_decode_kernel_shapes(gpu):
     _check("decode 16 rows on one kv head", q, k, v, scale=SCALE, kv_len=4990)
     q, k, v = O.make_inputs(44, T=2, Hq=64, Hkv=8, n_kv=1024)
     _check("verify T=2 gqa 8:1 (16 rows)", q, k, v, scale=SCALE, kv_len=1000, causal_pos0=998)
+
+
+def test_decode_kernel_two_row_blocks(gpu):
+    # 17..32 query rows per kv head with implicit masks: the decode kernel's
+    # two-row-block form (8-draft verify), with sinks, softcap, two streams,
+    # ragged row counts and a kv_len inside the last stage
+    rng = np.random.default_rng(61)
+    q, k, v = O.make_inputs(61, T=8, Hq=32, Hkv=8, n_kv=2304)
+    sinks = rng.standard_normal(32).astype(np.float32) * 3
+    _check("two row blocks, sinks", q, k, v, None, sinks, scale=SCALE, kv_len=2056, causal_pos0=2048)
+    _check("two row blocks, softcap", q, k, v, scale=SCALE * 4, logit_softcap=5.0, kv_len=2056, causal_pos0=2048)
+    q, k, v = O.make_inputs(62, B=2, T=5, Hq=16, Hkv=4, n_kv=1500)
+    _check("two row blocks, 2 streams, 20 rows", q, k, v, scale=SCALE, kv_len=1493, causal_pos0=1488)
+    q, k, v = O.make_inputs(63, T=3, Hq=56, Hkv=7, n_kv=700)
+    _check("two row blocks, 24 rows, G 8", q, k, v, scale=SCALE, kv_len=650)
