@@ -9,21 +9,20 @@
 // (sumi * d_w) * d_x with sumi the integer dot product of the block's
 // weights minus 8 and its Q8_0 values (nnml_vec_dot_q4_0_q8_0, arm.cpp:401).
 //
-// Two kernels:
-//   quantize_q8_kernel  one thread per (token, 32-value block): the block's
-//                       int8 values (kept aligned, [T][K]), its scale as
-//                       the f16-rounded value in f32, and the sum of its
-//                       values (so the weights' offset of 8 becomes one
-//                       multiply per block instead of a subtract per byte);
-//   gemv_q4_kernel      one wavefront per output row: lane l takes the
-//                       row's blocks l*BPL .. l*BPL + BPL - 1, a contiguous
-//                       36-byte-aligned chunk of 18-byte blocks, keeps them
-//                       in registers for every token, and forms each
-//                       block's dot product with 8 v_dot4_i32_i8 on the
-//                       unsigned nibbles; lane partial sums meet in a wave
-//                       reduction.
-// Decode and speculative verify (T <= 64 tokens) stream the 4-bit weights
-// once: HBM-bound, 18 bytes per 32 weights.
+// Up to 8 tokens (decode, speculative verify) take one launch,
+// gemv_q4_fused_kernel: one wavefront per output row, every row resident at
+// once; each workgroup issues its rows' weight loads, quantizes all T
+// activation rows into LDS meanwhile (the activations are small and
+// L2-resident), then lane l forms the dot products of the row's blocks
+// l*BPL .. l*BPL + BPL - 1 (a contiguous 36-byte-aligned run of 18-byte
+// blocks held in registers) with 8 v_dot4_i32_i8 per block on the unsigned
+// nibbles, the weights' offset of 8 folded into one multiply by the block's
+// value sum; lane sums meet in a DPP wave reduction.
+// Longer inputs (up to 64 tokens) take two launches: quantize_q8_kernel
+// (one thread per (token, block), into grow-only library scratch) and
+// gemv_q4_kernel (the same dot products, activations from that scratch).
+// Either way the 4-bit weights stream once: HBM-bound, 18 bytes per 32
+// weights.
 
 #include <hip/hip_runtime.h>
 
