@@ -8,10 +8,11 @@
 // Wave w takes row half w & 1 (32 rows: 2 MFMA row blocks, so each K/V
 // operand read from LDS feeds 2 MFMAs) and cell split w >> 1 (every 4th
 // 32-cell tile of the visible range). The two waves of a split sit on
-// different SIMDs and share the split's ring of two 16 KiB LDS stages: one of
-// them (row half 0 for splits 0 and 1, row half 1 for splits 2 and 3, so that
-// each SIMD hosts one) loads the tiles, publishes "tile landed" in an LDS
-// flag, and refills a stage once the other has published "tile read".
+// different SIMDs and share the split's ring of two 16 KiB LDS stages: each
+// loads half of every tile, publishes "my half landed" in an LDS flag, reads
+// the whole tile once the other's half has landed, publishes "stage read",
+// and refills its half of the stage once the other has read it too. (With
+// one wave loading whole tiles the other waited for it on every tile.)
 // No workgroup barrier runs in the loop, so the splits drift apart and the
 // two waves on each SIMD (different splits) overlap each other's matrix and
 // vector work. A 512-token chunk of Qwen3-4B gives 32 row tiles x 8 kv heads
@@ -25,8 +26,8 @@
 //     at slot j ^ (c & 15), read transposed by ds_read_b64_tr_b16 into V^T
 //     A operands whose k slots follow the S^T output layout (cells 4g + i
 //     and 16 + 4g + i of lane group g), so P^T is S^T in place.
-// The DMA is inline assembly the compiler does not count; the loading wave
-// waits for its tile (s_waitcnt vmcnt) before publishing it. The query rows
+// The DMA is inline assembly the compiler does not count; each wave waits
+// for its own half (s_waitcnt vmcnt) before publishing it. The query rows
 // come the same way, once per workgroup, into a staging area that holds the
 // flags afterwards.
 //
@@ -71,17 +72,18 @@ struct TileOps {
     half8 vt[8];                             // V^T A operands, dim block d
 };
 
-// LDS-DMA of tile (cells cb ..) into a stage: 8 K blocks, then 8 V blocks.
-__device__ __forceinline__ void issue_tile(const int4v kd, const int4v vd, const uint32_t base, const uint32_t cb,
-                                           const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n) {
-    const uint32_t kofs = (cb + (uint32_t) n) * k_nb1 + (uint32_t) (g * 16);
+// LDS-DMA of half h of tile (cells cb ..) into a stage: the 4 K blocks of
+// cell block mb = h, then V blocks 4h .. 4h + 3 (cells 16h .. 16h + 15).
+__device__ __forceinline__ void issue_half(const int4v kd, const int4v vd, const uint32_t base, const uint32_t cb,
+                                           const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n,
+                                           const int h) {
+    const uint32_t kofs = (cb + (uint32_t) n) * k_nb1 + (uint32_t) (g * 16) + (uint32_t) (16 * h) * k_nb1;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
+    for (int kb = 0; kb < 4; ++kb)
+        dma16(kd, kofs + (uint32_t) (64 * kb), base + (uint32_t) ((h * 4 + kb) * 1024));
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-            dma16(kd, kofs + (uint32_t) (16 * mb) * k_nb1 + (uint32_t) (64 * kb), base + (uint32_t) ((mb * 4 + kb) * 1024));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int ii = 0; ii < 4; ++ii) {
+        const int i = 4 * h + ii;
         const int c = 4 * i + g;
         dma16(vd, (cb + (uint32_t) c) * v_nb1 + (uint32_t) (((n ^ c) & 15) * 16), base + (uint32_t) (kKBytes + i * 1024));
     }
@@ -131,15 +133,16 @@ __device__ __forceinline__ int tile_cell(const int cb0, const int it, const int 
     return cb0 + (j < nt ? j : j - nt) * kStride;
 }
 
-// After the softmax of tile it, the loading wave refills the tile's stage
-// with tile it + 2 once the other wave has read it.
-__device__ __forceinline__ bool refill(const bool loader, const int it, const int nt, const int rot, const int * done,
+// After the softmax of tile it, a wave refills its half of the tile's stage
+// with tile it + 2 once the other wave has read the stage (its own reads are
+// complete: the wave waited for them before publishing its own "read").
+__device__ __forceinline__ bool refill(const int h, const int it, const int nt, const int rot, const int * done,
                                        const int4v kd, const int4v vd, const uint32_t ring_addr, const int cb0,
                                        const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n) {
-    if (!loader || it + 2 >= nt) return true;
+    if (it + 2 >= nt) return true;
     const bool ok = flag_wait(done, it);
-    if (ok) issue_tile(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) tile_cell(cb0, it + 2, rot, nt),
-                       k_nb1, v_nb1, g, n);
+    if (ok) issue_half(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) tile_cell(cb0, it + 2, rot, nt),
+                       k_nb1, v_nb1, g, n, h);
     return ok;
 }
 
@@ -209,10 +212,6 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int rot = nt > 0 ? (int) (((int64_t) rt * nt) / p.n_row_tiles) : 0;
     const char * ring = &lds[cs * kNB * kStage];
     const uint32_t ring_addr = lds_addr(ring);
-    // wave w runs on SIMD w % 4: splits 0 and 2 share SIMDs 0 and 1, splits 1
-    // and 3 SIMDs 2 and 3; the loading wave alternates between the row halves
-    // so that every SIMD hosts one loader and one reader
-    const bool loader = rh == ((cs >> 1) & 1);
 
     // The tile's query rows travel once, by LDS-DMA into the staging area
     // behind the rings, ahead of the first K/V tiles: wave w loads rows
@@ -232,10 +231,9 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
                   lds_addr(qst) + (uint32_t) ((8 * wave + 2 * i) * 512));
         }
     }
-    if (loader && nt > 0) issue_tile(kd, vd, ring_addr, (uint32_t) tile_cell(cb0, 0, rot, nt), k_nb1, v_nb1, g, n);
-    if (loader && nt > 1)
-        issue_tile(kd, vd, ring_addr + kStage, (uint32_t) tile_cell(cb0, 1, rot, nt), k_nb1, v_nb1, g, n);
-    wait_later<2, 16>(loader ? min(nt, 2) : 0);                      // own query rows landed
+    if (nt > 0) issue_half(kd, vd, ring_addr, (uint32_t) tile_cell(cb0, 0, rot, nt), k_nb1, v_nb1, g, n, rh);
+    if (nt > 1) issue_half(kd, vd, ring_addr + kStage, (uint32_t) tile_cell(cb0, 1, rot, nt), k_nb1, v_nb1, g, n, rh);
+    wait_later<2, 8>(min(nt, 2));                                     // own query rows landed
     __syncthreads();                                                   // everyone's
 
     // query rows held by this lane (column n of its two row blocks) and their
@@ -257,13 +255,15 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             qf[rb][kb] = rvalid[rb] ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
         }
     }
-    // the staging area becomes the flags: landed[cs], then done[cs]
+    // the staging area becomes the flags: landed[cs][rh], then done[cs][rh]
     int * flags = (int *) qst;
     __syncthreads();
-    if (threadIdx.x < 2 * kCS) flags[threadIdx.x] = -1;
+    if (threadIdx.x < 4 * kCS) flags[threadIdx.x] = -1;
     __syncthreads();
-    int * landed = flags + cs;
-    const int * done = flags + kCS + cs;
+    int * landed = flags + 2 * cs + rh;                               // own half landed
+    const int * landed_o = flags + 2 * cs + (rh ^ 1);                 // the other wave's half
+    int * done_m = flags + 2 * kCS + 2 * cs + rh;                     // own reads of the stage done
+    const int * done = flags + 2 * kCS + 2 * cs + (rh ^ 1);
 
     int lim[kPRB];
 #pragma unroll
@@ -304,11 +304,10 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     int it = 0;
     while (it < nt && ok) {
         for (; it < nt; ++it) {
-            // tile it in its stage: landed (own loads, or the loader's flag)
-            if (loader) {
-                wait_later<1, 16>(it + 1 < nt ? 1 : 0);
-                flag_set(landed, it);
-            } else if (!flag_wait(landed, it)) {
+            // tile it in its stage: own half landed (vmcnt), the other's by its flag
+            wait_later<1, 8>(it + 1 < nt ? 1 : 0);
+            flag_set(landed, it);
+            if (!flag_wait(landed_o, it)) {
                 ok = false;
                 break;
             }
@@ -316,7 +315,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             mem_barrier();
             __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));                 // lgkmcnt(0): the stage is read
             mem_barrier();
-            if (!loader) flag_set(landed + kCS, it);                       // done[cs]
+            flag_set(done_m, it);
             const int cb = tile_cell(cb0, it, rot, nt);
 
             // S^T = K Q^T: cells 4g+i (mb 0) and 16+4g+i (mb 1) of row n
@@ -363,7 +362,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             }
             if (__any(grow_any)) break;
             accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-            if (!refill(loader, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
+            if (!refill(rh, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
                 ok = false;
                 break;
             }
@@ -382,7 +381,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
             m_run[rb] = mn;
         }
         accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-        ok = refill(loader, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
+        ok = refill(rh, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
         ++it;
     }
     if (!ok && lane == 0) atomicOr(p.err + 2, 1);                      // reported by al_device_errors
