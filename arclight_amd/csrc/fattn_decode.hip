@@ -385,16 +385,31 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     order_after_counter();
     if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
 
-    // Last workgroup: two adjacent lanes per (row, 4 dims), each taking 16
-    // of the at most 32 splits, then combining with its partner (split half
-    // 0 first, on both lanes). A thread takes two such items per round (one
-    // with two row blocks, for registers) with all of their loads in flight,
-    // so a decode merge (4 rows = 256 items) is one round trip.
+    // Last workgroup. The (m, l) pair of every (row, split) is loaded once
+    // (thread i takes pairs i, i + 64 WS, ...) and shared through LDS; the
+    // output items are two adjacent lanes per (row, 4 dims), each taking 16
+    // of the at most 32 splits and then combining with its partner (split
+    // half 0 first, on both lanes). A thread takes two items per round (one
+    // with two row blocks, for registers); the first round's O loads are
+    // issued before the pairs go to LDS, so a decode merge (4 rows = 256
+    // items) is one round trip.
     constexpr int kHalf = kMaxSplit / 2;
     constexpr int kItems = RB == 1 ? 2 : 1;                            // items per thread and round (registers)
+    constexpr int kPairs = (16 * RB * kMaxSplit + WS * 64 - 1) / (WS * 64);
+    float2 * ml_s = (float2 *) &lds[0][0][0];                          // [row][kMaxSplit]; the rings are free
+    const int n_pairs = rows_here * kMaxSplit;
+    // (loads are unconditional, from clamped in-range addresses, and the
+    // unused ones are replaced afterwards: no branch, so the O loads below
+    // stay in flight while the pairs are stored)
+    float2 mlv[kPairs];
+#pragma unroll
+    for (int i = 0; i < kPairs; ++i) {
+        const int pi = i * WS * 64 + threadIdx.x;
+        const int rr = min(pi / kMaxSplit, rows_here - 1), sp = min(pi % kMaxSplit, p.n_split - 1);
+        mlv[i] = buf_load8_dev(pr, (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4 + 128 * 4));
+    }
     const int n_items = rows_here * 64;
     for (int base = 0; base < n_items; base += kItems * WS * 64) {
-        float2 ml[kItems][kHalf];
         float4 ov[kItems][kHalf];
 #pragma unroll
         for (int it2 = 0; it2 < kItems; ++it2) {
@@ -404,34 +419,42 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int rr = idx < n_items ? idx >> 6 : 0;
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
-                const int sp = half * kHalf + j;
-                if (sp < p.n_split) {
-                    const uint32_t row = (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4);
-                    ml[it2][j] = buf_load8_dev(pr, row + 128 * 4);
-                    ov[it2][j] = buf_load16_dev(pr, row + d4 * 16);
-                } else {
-                    ml[it2][j] = float2{-AL_INF, 0.0f};
-                    ov[it2][j] = float4{0, 0, 0, 0};
-                }
+                const int sp = min(half * kHalf + j, p.n_split - 1);
+                ov[it2][j] = buf_load16_dev(pr, (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4 + d4 * 16));
             }
+        }
+        if (base == 0) {
+            // the pairs into LDS (LDS only: no wait for the O loads in flight)
+#pragma unroll
+            for (int i = 0; i < kPairs; ++i) {
+                const int pi = i * WS * 64 + threadIdx.x;
+                ml_s[pi] = (pi % kMaxSplit) < p.n_split ? mlv[i] : float2{-AL_INF, 0.0f};
+            }
+            mem_barrier();
+            __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0)
+            __builtin_amdgcn_s_barrier();
+            mem_barrier();
         }
 #pragma unroll
         for (int it2 = 0; it2 < kItems; ++it2) {
             const int idx = base + it2 * WS * 64 + threadIdx.x;
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
-            const int rr = idx >> 6;
-            float Mh = ml[it2][0].x;
+            const int rr = idx < n_items ? idx >> 6 : 0;
+            float2 ml[kHalf];
 #pragma unroll
-            for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[it2][j].x);
+            for (int j = 0; j < kHalf; ++j) ml[j] = ml_s[rr * kMaxSplit + half * kHalf + j];
+            float Mh = ml[0].x;
+#pragma unroll
+            for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[j].x);
             const float M = fmaxf(Mh, __shfl_xor(Mh, 1));
             const float Mu = (M == -AL_INF) ? 0.0f : M;
             float Lh = 0.0f;
             float4 ah = {0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
-                const float w = exp_fast(ml[it2][j].x - Mu);
-                Lh += w * ml[it2][j].y;
+                const float w = exp_fast(ml[j].x - Mu);
+                Lh += w * ml[j].y;
                 ah.x += w * ov[it2][j].x; ah.y += w * ov[it2][j].y; ah.z += w * ov[it2][j].z; ah.w += w * ov[it2][j].w;
             }
             const float Lo = __shfl_xor(Lh, 1);
