@@ -309,7 +309,7 @@ def load_traffic(kernel, ctx):
 def main():
     a = parse()
     if a.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+        print(json.dumps({"error": "bench.py runs on one GPU only; --gpus must be 1 "
                           "(attention would shard by KV head across GPUs, with no exchange before "
                           "the output projection)"}))
         sys.exit(2)

@@ -2,7 +2,7 @@
  * fattn_oracle.c - CPU oracle for ArcLight's flash-attention op.
  *
  * TEST INFRASTRUCTURE ONLY: loaded by tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py, as the checker or the timed CPU baseline.
+ * cpu_baseline leg of bench.py, as the reference results or the timed CPU baseline.
  * Nothing in the product path links or calls this file.
  *
  * Restated from (paths relative to the ArcLight tree):

@@ -3,7 +3,7 @@
  * INFRASTRUCTURE ONLY).
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker or the CPU baseline. The
+ * load this library, and only as the reference results or the CPU baseline. The
  * product path (arclight_amd, libarclight_fattn.so) never calls it.
  *
  * Three restatements of ArcLight's nnml_compute_forward_flash_attn_ext_f16

@@ -1,5 +1,5 @@
 """Oracle of the KV-cache cell bookkeeping and attention mask (test
-infrastructure only: the tests use it as the checker, nothing ships it).
+infrastructure only: the tests compare against it, nothing ships it).
 
 A plain-Python restatement of ArcLight's llm_kv_cells / llm_kv_cache logic
 for the f16 flash-attention cache (FA on: V not transposed):

@@ -1,7 +1,7 @@
 """Python binding of the CPU oracle (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, as the checker or as the timed CPU baseline. The product package
+this module, as the reference results or as the timed CPU baseline. The product package
 (arclight_amd) never imports it.
 
 Arrays use the physical layouts documented in arclight_amd.abi:
