@@ -1,0 +1,90 @@
+"""Parity at the benchmark shapes themselves: Qwen3-8B-shape speculative
+verify over an 8192-cell context, Qwen3-32B-shape decode at 32768 cells and
+prefill in 1024-token causal chunks, plus a size-independent property of
+the full 2048-token Qwen3-4B prefill: its four causal chunks of 512 equal
+one causal call over all 2048 tokens.
+
+Where the oracle over every row of a call would take minutes (a 1024-token
+chunk at 64 query heads), the device computes the whole call and a sample of
+its tokens is compared with the oracle run on those tokens alone: rows are
+independent (nnml/src/ops/arm/arm.cpp:2287-2291 forms each (token, head)
+row from its q row, K, V and its own mask row), so the oracle gets the
+sampled q rows with their rows of the same causal mask.
+
+Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the fp32 output against oracle
+O2, as everywhere.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.fattn_cases import assert_parity, run_gpu
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / math.sqrt(128)
+
+
+def _case(name):
+    print(f"\n[case] {name}", flush=True)
+
+
+def _sampled_ref(q, k, v, sel, pos0, kv_len):
+    """Oracle rows of tokens `sel` of a causal call whose token t sits at
+    position pos0 + t over cells [0, kv_len)."""
+    T, n_kv = q.shape[1], k.shape[1]
+    full = O.causal_mask(T, n_kv, pos0, kv_len=kv_len)
+    rows = (len(sel) + 63) // 64 * 64
+    m = np.full((1, 1, rows, n_kv), -np.inf, dtype=np.float16)
+    m[:, :, :len(sel)] = full[:, :, sel]
+    return O.attention(np.ascontiguousarray(q[:, sel]), k, v, m, scale=SCALE)
+
+
+@pytest.mark.parametrize("T", [4, 8])
+def test_verify_qwen3_8b_ctx8192(gpu, T):
+    # drafts at positions 8192 .. 8192 + T - 1, cells padded to 256
+    C = 8192
+    n_kv = (C + T + 255) // 256 * 256
+    q, k, v = O.make_inputs(8192 + T, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    _case(f"verify T={T} ctx {C} implicit")
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=C + T, causal_pos0=C)
+    assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=C + T, causal_pos0=C), ref, what=f"verify T={T} implicit")
+    _case(f"verify T={T} ctx {C} explicit mask")
+    got = run_gpu(q, k, v, O.causal_mask(T, n_kv, C, kv_len=C + T), scale=SCALE)
+    assert_parity(got, ref, what=f"verify T={T} explicit")
+
+
+def test_decode_qwen3_32b_ctx32768(gpu):
+    q, k, v = O.make_inputs(3232, T=1, Hq=64, Hkv=8, n_kv=32768)
+    _case("decode Qwen3-32B shape ctx 32768")
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=32768)
+    assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=32768), ref, what="decode 32B ctx 32768")
+
+
+@pytest.mark.parametrize("pos0", [0, 3072])
+def test_prefill_qwen3_32b_chunk1024(gpu, pos0):
+    # first and last 1024-token chunk of a 4096-token prompt at 64 query heads
+    T, kv_len = 1024, pos0 + 1024
+    q, k, v = O.make_inputs(1024 + pos0, T=T, Hq=64, Hkv=8, n_kv=kv_len)
+    _case(f"prefill Qwen3-32B shape chunk 1024 pos0 {pos0}")
+    got = run_gpu(q, k, v, scale=SCALE, kv_len=kv_len, causal_pos0=pos0)
+    rng = np.random.default_rng(pos0)
+    sel = np.unique(np.concatenate([[0, 1, 63, 64, T - 1], rng.choice(T, 27, replace=False)]))
+    ref = _sampled_ref(q, k, v, sel, pos0, kv_len)
+    assert_parity(got[:, sel], ref, what=f"prefill 32B chunk pos0 {pos0} ({len(sel)} tokens)")
+
+
+def test_prefill_chunks_equal_one_causal_call(gpu):
+    # 2048-token Qwen3-4B-shape prompt: 4 chunks of 512 (chunk c sees cells
+    # [0, 512 (c + 1))) against one causal call over all 2048 tokens
+    q, k, v = O.make_inputs(2048, T=2048, Hq=32, Hkv=8, n_kv=2048)
+    _case("prefill 2048 one causal call")
+    whole = run_gpu(q, k, v, scale=SCALE, kv_len=2048, causal_pos0=0)
+    sel = np.array([0, 511, 512, 1000, 1535, 1536, 2047])
+    assert_parity(whole[:, sel], _sampled_ref(q, k, v, sel, 0, 2048), what="one causal call, sampled rows")
+    for c in range(4):
+        _case(f"prefill 2048 chunk {c}")
+        qc = np.ascontiguousarray(q[:, 512 * c:512 * (c + 1)])
+        got = run_gpu(qc, k, v, scale=SCALE, kv_len=512 * (c + 1), causal_pos0=512 * c)
+        assert_parity(got, whole[:, 512 * c:512 * (c + 1)], what=f"chunk {c} vs one call")
