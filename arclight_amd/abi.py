@@ -152,6 +152,16 @@ class AlRopeParams(ctypes.Structure):
     ]
 
 
+class AlAttnInputsArgs(ctypes.Structure):
+    """al_attn_inputs_args (include/arclight_prologue.h)."""
+    _fields_ = [
+        ("q", AlTensor), ("q_w", AlTensor), ("k", AlTensor), ("k_w", AlTensor), ("v", AlTensor),
+        ("pos", AlTensor), ("rows", AlTensor), ("q_out", AlTensor), ("k_cache", AlTensor), ("v_cache", AlTensor),
+        ("eps", ctypes.c_float),
+        ("rope", ctypes.POINTER(AlRopeParams)),
+    ]
+
+
 def qwen3_rope(n_ctx_orig=40960):
     """Qwen3's rope_ext parameters (models/qwen3.cpp:49-55)."""
     return AlRopeParams(128, AL_ROPE_NEOX, n_ctx_orig, 1000000.0, 1.0, 0.0, 1.0, 32.0, 1.0)

@@ -13,31 +13,7 @@
 namespace {
 
 __global__ __launch_bounds__(256) void set_rows_kernel(const SetRowsParams p) {
-    const int i = blockIdx.x;          // source row
-    const int i02 = blockIdx.y;
-    const int i03 = blockIdx.z;
-    const int i12 = i03 % p.i_ne2;
-    const int i11 = i02 % p.i_ne1;
-    const char * ip = p.idx + (int64_t) i * p.i_nb0 + (int64_t) i11 * p.i_nb1 + (int64_t) i12 * p.i_nb2;
-    const int64_t i1 = p.idx64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
-    if (i1 < 0 || i1 >= p.n_dst) {
-        if (threadIdx.x == 0) {
-            if (atomicCAS(p.err, 0, 1) == 0) p.err[1] = (int) i1;
-        }
-        return;
-    }
-    const float * src = (const float *) (p.src + (int64_t) i * p.s_nb1 + (int64_t) i02 * p.s_nb2 + (int64_t) i03 * p.s_nb3);
-    _Float16 * dst = (_Float16 *) (p.dst + i1 * p.d_nb1 + (int64_t) i02 * p.d_nb2 + (int64_t) i03 * p.d_nb3);
-    if (p.vec4) {
-        for (int c = 4 * threadIdx.x; c < p.nc; c += 4 * blockDim.x) {
-            const float4 x = *(const float4 *) (src + c);
-            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-            half4 h = {(_Float16) x.x, (_Float16) x.y, (_Float16) x.z, (_Float16) x.w};
-            *(half4 *) (dst + c) = h;
-        }
-    } else {
-        for (int c = threadIdx.x; c < p.nc; c += blockDim.x) dst[c] = (_Float16) src[c];
-    }
+    set_rows_row(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 }  // namespace
@@ -48,7 +24,8 @@ hipError_t set_rows_launch(const SetRowsParams & p, hipStream_t stream) {
     return hipGetLastError();
 }
 
-extern "C" int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src, const al_tensor * idx, void * stream) {
+int set_rows_params(const al_tensor * dst, const al_tensor * src, const al_tensor * idx, SetRowsParams * out, bool * empty) {
+    *empty = false;
     if (!dst || !src || !idx || !dst->data || !src->data || !idx->data)
         return al_fail(AL_ERR_INVALID, "set_rows: dst, src and idx are required");
     if (src->type != AL_TYPE_F32)
@@ -63,7 +40,10 @@ extern "C" int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
         return al_fail(AL_ERR_INVALID, "set_rows: index tensor does not broadcast over src");
     if (idx->ne[0] < src->ne[1]) return al_fail(AL_ERR_INVALID, "set_rows: fewer indices than rows");
     if (src->nb[0] != 4 || dst->nb[0] != 2) return al_fail(AL_ERR_INVALID, "set_rows: rows must be contiguous");
-    if (src->ne[1] == 0 || src->ne[2] == 0 || src->ne[3] == 0) return AL_OK;
+    if (src->ne[1] == 0 || src->ne[2] == 0 || src->ne[3] == 0) {
+        *empty = true;
+        return AL_OK;
+    }
     if (src->ne[1] > INT32_MAX || src->ne[2] > 65535 || src->ne[3] > 65535 || src->ne[0] > INT32_MAX)
         return al_fail(AL_ERR_UNSUPPORTED, "set_rows: sizes out of range");
     int * err = nullptr;
@@ -82,6 +62,15 @@ extern "C" int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
                       dst->nb[1] % 8 == 0 && dst->nb[2] % 8 == 0 && dst->nb[3] % 8 == 0 && (src->ne[0] % 4) == 0;
     p.vec4 = al16 ? 1 : 0;
     p.err = err;
+    *out = p;
+    return AL_OK;
+}
+
+extern "C" int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src, const al_tensor * idx, void * stream) {
+    SetRowsParams p;
+    bool empty = false;
+    const int rc = set_rows_params(dst, src, idx, &p, &empty);
+    if (rc != AL_OK || empty) return rc;
     const hipError_t e = set_rows_launch(p, (hipStream_t) stream);
     if (e != hipSuccess) return al_hip_fail(e, "set_rows: kernel launch");
     return AL_OK;

@@ -21,6 +21,7 @@
 #include <cstring>
 
 #include "../../include/arclight_prologue.h"
+#include "kv_write.hpp"
 #include "runtime.hpp"
 
 namespace {
@@ -45,16 +46,14 @@ __device__ __forceinline__ double wave_sum(double v) {
     return v;
 }
 
-// MODE: 0 no rotation, 1 pairs (2i, 2i + 1), 2 NEOX pairs (i, i + 64).
+// Row (head h, token t), one wavefront. MODE: 0 no rotation, 1 pairs
+// (2i, 2i + 1), 2 NEOX pairs (i, i + 64).
 template <int MODE, bool CACHE>
-__global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) {
+__device__ __forceinline__ void norm_rope_row(const NormRopeParams & p, const int h, const int t, const int lane) {
     // every product and sum rounded on its own, as the reference's C source
     // reads: at angles of thousands of radians one ulp of theta moves the
     // output by ~1e-4, so a fused multiply-add there would not match
 #pragma clang fp contract(off)
-    const int lane = threadIdx.x & 63;
-    const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
-    const int t = blockIdx.x;
     if (h >= p.H) return;
 
     const int d0 = MODE == 1 ? 2 * lane : lane;
@@ -115,6 +114,24 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) 
     }
 }
 
+template <int MODE, bool CACHE>
+__global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) {
+    norm_rope_row<MODE, CACHE>(p, blockIdx.y * 4 + (threadIdx.x >> 6), blockIdx.x, threadIdx.x & 63);
+}
+
+// The attention inputs of one layer in one launch: blockIdx.y < yq are Q
+// rows (4 heads per workgroup), then yk of K rows into the cache, then one
+// workgroup per token for its V row.
+template <int MODE>
+__global__ __launch_bounds__(256) void attn_inputs_kernel(const NormRopeParams q, const NormRopeParams k,
+                                                          const SetRowsParams v, const int yq, const int yk) {
+    const int by = blockIdx.y;
+    const int hw = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (by < yq) norm_rope_row<MODE, false>(q, by * 4 + hw, blockIdx.x, lane);
+    else if (by < yq + yk) norm_rope_row<MODE, true>(k, (by - yq) * 4 + hw, blockIdx.x, lane);
+    else set_rows_row(v, blockIdx.x, 0, 0);
+}
+
 template <int MODE>
 hipError_t launch_mode(const NormRopeParams & p, bool cache, hipStream_t stream) {
     const dim3 grid((unsigned) p.T, (unsigned) ((p.H + 3) / 4));
@@ -129,11 +146,11 @@ float yarn_corr_dim(int n_dims, int n_ctx_orig, float n_rot, float base) {
     return n_dims * logf(n_ctx_orig / (n_rot * 2 * (float) pi)) / (2 * logf(base));
 }
 
-}  // namespace
-
-extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
-                                    const al_rope_params * rope, const al_tensor * y, const al_tensor * rows,
-                                    void * stream) {
+// Checks the operands as al_rms_norm_rope_f32 documents them and fills p
+// and the rotation mode (0 none, 1 normal, 2 NEOX).
+int norm_rope_params(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
+                     const al_rope_params * rope, const al_tensor * y, const al_tensor * rows, NormRopeParams * out,
+                     int * mode_out) {
     if (!x || !pos || !y) return al_fail(AL_ERR_INVALID, "rms_norm_rope: x, pos and y required");
     if (x->type != AL_TYPE_F32 || x->ne[0] != 128 || x->nb[0] != 4 || x->ne[3] != 1)
         return al_fail(AL_ERR_UNSUPPORTED, "rms_norm_rope: x must be f32 [128, H, T, 1] with nb0 = 4");
@@ -189,6 +206,21 @@ extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, co
     }
     p.y = (char *) y->data;
     if (!p.x || !p.y) return al_fail(AL_ERR_INVALID, "rms_norm_rope: null data");
+    *out = p;
+    *mode_out = mode;
+    return AL_OK;
+}
+
+}  // namespace
+
+extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
+                                    const al_rope_params * rope, const al_tensor * y, const al_tensor * rows,
+                                    void * stream) {
+    NormRopeParams p;
+    int mode = 0;
+    const int rc = norm_rope_params(x, w, pos, eps, rope, y, rows, &p, &mode);
+    if (rc != AL_OK) return rc;
+    const bool cache = rows != nullptr;
     hipStream_t s = (hipStream_t) stream;
     hipError_t e;
     switch (mode) {
@@ -197,4 +229,32 @@ extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, co
         default: e = launch_mode<0>(p, cache, s); break;
     }
     return e == hipSuccess ? AL_OK : al_hip_fail(e, "rms_norm_rope: launch");
+}
+
+extern "C" int al_attn_inputs_f32(const al_attn_inputs_args * a, void * stream) {
+    if (!a) return al_fail(AL_ERR_INVALID, "attn_inputs: null arguments");
+    NormRopeParams q, k;
+    int mq = 0, mk = 0;
+    int rc = norm_rope_params(&a->q, a->q_w.data ? &a->q_w : nullptr, &a->pos, a->eps, a->rope, &a->q_out, nullptr, &q, &mq);
+    if (rc != AL_OK) return rc;
+    rc = norm_rope_params(&a->k, a->k_w.data ? &a->k_w : nullptr, &a->pos, a->eps, a->rope, &a->k_cache, &a->rows, &k, &mk);
+    if (rc != AL_OK) return rc;
+    if (q.T != k.T) return al_fail(AL_ERR_INVALID, "attn_inputs: q has %d tokens, k %d", q.T, k.T);
+    if (a->v.ne[1] != q.T || a->v.ne[2] != 1 || a->v.ne[3] != 1)
+        return al_fail(AL_ERR_INVALID, "attn_inputs: v must be f32 [n, T] with the tokens of q");
+    SetRowsParams v;
+    bool empty = false;
+    rc = set_rows_params(&a->v_cache, &a->v, &a->rows, &v, &empty);
+    if (rc != AL_OK) return rc;
+    if (empty) return al_fail(AL_ERR_INVALID, "attn_inputs: empty v");
+    const int yq = (q.H + 3) / 4, yk = (k.H + 3) / 4;
+    const dim3 grid((unsigned) q.T, (unsigned) (yq + yk + 1));
+    hipStream_t s = (hipStream_t) stream;
+    switch (mq) {
+        case 2: hipLaunchKernelGGL(attn_inputs_kernel<2>, grid, dim3(256), 0, s, q, k, v, yq, yk); break;
+        case 1: hipLaunchKernelGGL(attn_inputs_kernel<1>, grid, dim3(256), 0, s, q, k, v, yq, yk); break;
+        default: hipLaunchKernelGGL(attn_inputs_kernel<0>, grid, dim3(256), 0, s, q, k, v, yq, yk); break;
+    }
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? AL_OK : al_hip_fail(e, "attn_inputs: launch");
 }

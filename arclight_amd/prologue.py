@@ -8,6 +8,10 @@ is the node chain rms_norm -> mul -> rope_ext (nnml/src/ops/ops.cpp:680-726,
 1248-1250, 871-962), the second form followed by cpy_k's set_rows into the
 f16 cache (ops.cpp:135-181). Operands are DeviceTensors in nnml order:
 qcur / kcur (T, H, 128) f32, pos (T,) int32, rows (T,) int64.
+
+    attn_inputs(qcur, q_norm_w, kcur, k_norm_w, vcur, pos, rows, q_out, k_cache, v_cache, eps=eps, rope=...)
+
+does both of those and the V write (cpy_v's set_rows) in one launch.
 """
 import ctypes
 
@@ -32,3 +36,22 @@ def rms_norm_rope(x, w, pos, *, eps, rope=None, y=None, rows=None, stream=None):
          eps, ctypes.byref(rope) if rope is not None else None, ctypes.byref(yd),
          ctypes.byref(rd) if rd is not None else None, stream.handle if stream is not None else None)
     return y
+
+
+def attn_inputs(q, q_w, k, k_w, v, pos, rows, q_out, k_cache, v_cache, *, eps, rope=None, stream=None):
+    """Enqueues Q into q_out, K into k_cache and V into v_cache (at cache
+    rows `rows`) as one kernel; same results as rms_norm_rope for Q and K
+    and set_rows for V. v is an f32 (T, n) DeviceTensor."""
+    a = abi.AlAttnInputsArgs()
+    a.q, a.k, a.v = q.desc(), k.desc(), v.desc()
+    if q_w is not None:
+        a.q_w = q_w.desc()
+    if k_w is not None:
+        a.k_w = k_w.desc()
+    a.pos, a.rows = pos.desc(), rows.desc()
+    a.q_out, a.k_cache, a.v_cache = q_out.desc(), k_cache.desc(), v_cache.desc()
+    a.eps = eps
+    if rope is not None:
+        a.rope = ctypes.pointer(rope)
+    call("al_attn_inputs_f32", ctypes.byref(a), stream.handle if stream is not None else None)
+    return q_out

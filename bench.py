@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the 4K/16K decode, 8K verify and Qwen3-32B-shape lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
-    ap.add_argument("--only", choices=["decode", "prefill", "wo", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "wo", "copy", "step"], default=None,
                     help="run one workload only (for profiling); prints its own JSON line")
     return ap.parse_args()
 
@@ -183,7 +183,9 @@ def bench_other_configs(lib, stream, a):
     (Qwen3-8B attention shape = Qwen3-4B's), and the Qwen3-32B shape (64
     query heads, 64 layers) for decode at 32K and 4096-token prefill in
     1024-token chunks; then the attention output projection (Q4_0 WO) that
-    consumes the attention output, for decode and an 8-token verify."""
+    consumes the attention output, for decode and an 8-token verify; last,
+    the whole attention block of a decode token (producers, K/V write,
+    attention, WO) per layer, replayed as one graph."""
     out = []
     steps = max(2, a.steps // 2)
 
@@ -213,6 +215,13 @@ def bench_other_configs(lib, stream, a):
                     "hbm_peak_frac": round(r["gbs"] / HBM_PEAK_GBS, 4),
                     "us_per_op": round(r["op_ms_mean"] * 1e3, 2)})
         print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
+    ms = bench_decode_step(lib, stream, a, ctx=32768, L=36, steps=steps)
+    out.append({"workload": "decode attention block per token (Q/K RMSNorm + rope, K/V write into the HBM ring, "
+                            "attention at the run-time length, Q4_0 WO), Qwen3-4B shape, context 32768, 36 layers, "
+                            "one replayed HIP graph",
+                "value": round(ms * 1e3 / 36, 2), "unit": "us/layer", "higher_is_better": False,
+                "tokens_per_s_attention_blocks": round(1e3 / ms, 1)})
+    print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
     return out
 
 
@@ -245,6 +254,68 @@ def bench_wo(lib, stream, a, K=4096, N=2560, T=1, copies=64, steps=None):
     byts = wo_bytes(K, N, T)
     return {"ms_per_step": ms, "bytes_per_launch": byts, "gbs": byts * copies / (ms * 1e-3) / 1e9,
             "op_ms_mean": ms / copies}
+
+
+def bench_decode_step(lib, stream, a, ctx=32768, L=36, steps=None, fused=True):
+    """One decode token through the attention block of every layer as the
+    Qwen3 graph runs it (qwen3.cpp:215-227, cgraph.cpp:485-500), captured
+    once as a HIP graph and replayed: Q and K RMSNorm + NEOX rope (K written
+    into the HBM ring at the token's cell), V written by set_rows, attention
+    over the ring's views at the run-time length {ctx + 1, ctx}, and the Q4_0
+    WO projection of the attention output. The three producers run as one
+    launch (al_attn_inputs_f32), or with fused=False as the three separate
+    ops. Returns ms per step (L layers)."""
+    from arclight_amd import abi, device, fattn, kv, matmul, prologue
+    from arclight_amd._lib import call
+    Hq, Hkv, D, N = 32, 8, 128, 2560
+    K = Hq * D
+    kv_size = (ctx + 1 + 255) // 256 * 256
+    rng = np.random.default_rng(a.seed + 11)
+    rope = abi.qwen3_rope()
+    ring = kv.KvRing(L, kv_size, Hkv, D, 1, 256, True)
+    try:
+        for il in range(L):
+            for j, which in enumerate("kv"):
+                call("al_util_fill_randn_f16", ring.cache_rows(il, which).ptr, kv_size * Hkv * D, a.seed,
+                     (2 * il + j + 7) << 40, None)
+        nb = K // 32
+        blocks = np.empty((N, nb, 18), np.uint8)
+        blocks[:] = rng.integers(0, 256, size=(N, nb, 18), dtype=np.uint8)
+        blocks[:, :, :2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+        wo = [matmul.Q4_0Matrix(blocks, K, N) for _ in range(L)]
+        wq = [device.DeviceTensor.from_numpy(rng.standard_normal(D).astype(np.float32)) for _ in range(L)]
+        wk = [device.DeviceTensor.from_numpy(rng.standard_normal(D).astype(np.float32)) for _ in range(L)]
+        qc = device.DeviceTensor.from_numpy(rng.standard_normal((1, Hq, D)).astype(np.float32))
+        kc = device.DeviceTensor.from_numpy(rng.standard_normal((1, Hkv, D)).astype(np.float32))
+        vc = device.DeviceTensor.from_numpy(rng.standard_normal((1, Hkv * D)).astype(np.float32))
+        pos = device.DeviceTensor.from_numpy(np.array([ctx], np.int32))
+        row = device.DeviceTensor.from_numpy(np.array([ctx], np.int64))
+        dyn = device.DeviceTensor.from_numpy(np.array([ctx + 1, ctx], np.int32))
+        qs = [device.DeviceTensor.empty((1, Hq, D), np.float32) for _ in range(L)]
+        att = [device.DeviceTensor.empty((1, 1, Hq, D), np.float32, axes=abi.DST_AXES) for _ in range(L)]
+        ys = [device.DeviceTensor.empty((1, N), np.float32) for _ in range(L)]
+        device.synchronize()
+
+        def enqueue():
+            for il in range(L):
+                if fused:
+                    prologue.attn_inputs(qc, wq[il], kc, wk[il], vc, pos, row, qs[il], ring.cache_rows(il, "k"),
+                                         ring.cache_rows(il, "v"), eps=1e-6, rope=rope, stream=stream)
+                else:
+                    prologue.rms_norm_rope(qc, wq[il], pos, eps=1e-6, rope=rope, y=qs[il], stream=stream)
+                    prologue.rms_norm_rope(kc, wk[il], pos, eps=1e-6, rope=rope, y=ring.cache_rows(il, "k"), rows=row,
+                                           stream=stream)
+                    fattn.set_rows(ring.cache_rows(il, "v"), vc, row, stream=stream)
+                qv = device.DeviceTensor(qs[il].buf, abi.AL_TYPE_F32, (1, 1, Hq, D), None, 0, abi.Q_AXES)
+                fattn.flash_attn_ext(qv, ring.get_k(il, kv_size), ring.get_v(il, kv_size), scale=1.0 / math.sqrt(D),
+                                     dst=att[il], kv_len=kv_size, causal_pos0=0, stream=stream, dyn_len=dyn)
+                matmul.mul_mat_q4_0(wo[il], device.DeviceTensor(att[il].buf, abi.AL_TYPE_F32, (1, K)), ys[il], stream)
+
+        ms = time_graph(lib, stream, None, steps or a.steps, a.warmup, enqueue)
+    finally:
+        device.synchronize()
+        ring.close()
+    return ms
 
 
 def bench_copy(stream, nbytes=1 << 30):
@@ -324,6 +395,13 @@ def main():
         return
     if a.only == "prefill":
         print(json.dumps({"prefill": bench_prefill(lib, stream, a)}))
+        return
+    if a.only == "step":
+        out = {}
+        for fused in (True, False):
+            ms = bench_decode_step(lib, stream, a, ctx=a.ctx, L=a.layers, fused=fused)
+            out["one_launch_inputs" if fused else "separate_inputs"] = {"ms_per_step": ms, "us_per_layer": ms * 1e3 / a.layers}
+        print(json.dumps({"step": out}))
         return
     if a.only == "wo":
         print(json.dumps({"wo": [bench_wo(lib, stream, a, K=K, N=N, T=T, copies=c)

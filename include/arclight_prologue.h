@@ -63,6 +63,36 @@ typedef struct al_rope_params {
 int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
                          const al_rope_params * rope, const al_tensor * y, const al_tensor * rows, void * stream);
 
+/*
+ * The three attention inputs of one layer in one launch: what
+ * al_rms_norm_rope_f32 does for Q (into q_out) and for K (into the K cache
+ * at rows[t]), and what al_set_rows_f32_f16 does for V (into the V cache at
+ * rows[t]), with the same results bit for bit. It replaces the node run of
+ * models/qwen3.cpp:211-227 up to attention (rms_norm -> mul -> rope_ext for
+ * Q and K, then cpy_k / cpy_v, nnml/src/cgraph.cpp:485-488) with one kernel,
+ * which saves two launch latencies per layer in a decode step. It has no
+ * single counterpart in the reference, which runs those nodes one by one.
+ * Operands as the two calls it replaces; v is f32 [n, T, 1, 1] with rows
+ * contiguous and one row per token of q. Out-of-range rows are not written
+ * and are reported by al_device_errors.
+ */
+typedef struct al_attn_inputs_args {
+    al_tensor q;        /* f32 [128, Hq, T, 1]   (Qcur) */
+    al_tensor q_w;      /* f32 [128] (ATTN_Q_NORM), or data NULL for none */
+    al_tensor k;        /* f32 [128, Hkv, T, 1]  (Kcur) */
+    al_tensor k_w;      /* f32 [128] (ATTN_K_NORM), or data NULL for none */
+    al_tensor v;        /* f32 [n, T]            (Vcur rows) */
+    al_tensor pos;      /* i32 [T], device       (inp_pos) */
+    al_tensor rows;     /* i64 / i32 [T], device: the cache row of each token (k_idxs / v_idxs) */
+    al_tensor q_out;    /* f32 [128, Hq, T] */
+    al_tensor k_cache;  /* f16 [128 * Hkv, n_rows] */
+    al_tensor v_cache;  /* f16 [n, n_rows] */
+    float eps;          /* RMSNorm epsilon */
+    const al_rope_params * rope;   /* NULL for no rotation */
+} al_attn_inputs_args;
+
+int al_attn_inputs_f32(const al_attn_inputs_args * a, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -152,3 +152,60 @@ def test_qwen3_layer_prologue_into_attention(gpu):
         ref = O.attention(q_ref[None], k_ref, v_ref, O.causal_mask(T, n_kv, p0, kv_len=p0 + T), scale=1 / math.sqrt(D))
         assert_parity(out.numpy(np.float32), ref, what=f"layer step {step}")
     ring.close()
+
+
+@pytest.mark.parametrize("T", [1, 7])
+def test_attn_inputs_one_launch_matches_the_separate_ops(gpu, T):
+    """al_attn_inputs_f32 writes Q, the K cache rows and the V cache rows bit
+    for bit as al_rms_norm_rope_f32 (Q; K with rows) and al_set_rows_f32_f16
+    (V) do one after another; rows outside the token's cells stay untouched."""
+    from arclight_amd import device, fattn, prologue
+    _case(f"attention inputs in one launch, T={T}")
+    Hq, Hkv, n_rows = 32, 8, 64
+    rng = np.random.default_rng(70 + T)
+    q, wq, pos = _inputs(71 + T, T, Hq)
+    k, wk, _ = _inputs(72 + T, T, Hkv)
+    v = (rng.standard_normal((T, Hkv * 128)) * 3).astype(np.float32)
+    rows = rng.choice(n_rows, T, replace=False).astype(np.int64)
+    rope = abi.qwen3_rope()
+    d = {n: device.DeviceTensor.from_numpy(a) for n, a in
+         (("q", q), ("k", k), ("v", v), ("wq", wq), ("wk", wk), ("pos", pos), ("rows", rows))}
+    caches = [[device.DeviceTensor.from_numpy(np.zeros((n_rows, Hkv * 128), np.uint16)) for _ in range(2)] for _ in range(2)]
+    q_outs = [device.DeviceTensor.empty((T, Hq, 128), np.float32) for _ in range(2)]
+    # the separate ops
+    prologue.rms_norm_rope(d["q"], d["wq"], d["pos"], eps=EPS, rope=rope, y=q_outs[0])
+    prologue.rms_norm_rope(d["k"], d["wk"], d["pos"], eps=EPS, rope=rope, y=caches[0][0], rows=d["rows"])
+    fattn.set_rows(caches[0][1], d["v"], d["rows"])
+    # one launch
+    prologue.attn_inputs(d["q"], d["wq"], d["k"], d["wk"], d["v"], d["pos"], d["rows"], q_outs[1], caches[1][0],
+                         caches[1][1], eps=EPS, rope=rope)
+    device.synchronize()
+    fattn.device_errors()
+    assert np.array_equal(q_outs[0].numpy(np.float32).view(np.uint32), q_outs[1].numpy(np.float32).view(np.uint32))
+    for j, what in enumerate(("K", "V")):
+        sep, one = caches[0][j].numpy(np.uint16), caches[1][j].numpy(np.uint16)
+        assert np.array_equal(sep, one), f"{what} cache differs"
+        assert not np.delete(one, rows, axis=0).any(), f"{what}: rows outside the tokens' cells written"
+        assert one[rows].any()
+
+
+def test_attn_inputs_bad_row_reported(gpu):
+    from arclight_amd import device, fattn, prologue
+    from arclight_amd._lib import ArclightError
+    _case("attention inputs, out-of-range cache row")
+    q, wq, pos = _inputs(80, 2, 4)
+    k, wk, _ = _inputs(81, 2, 2)
+    v = np.ones((2, 256), np.float32)
+    kc = device.DeviceTensor.from_numpy(np.zeros((10, 256), np.uint16))
+    vc = device.DeviceTensor.from_numpy(np.zeros((10, 256), np.uint16))
+    prologue.attn_inputs(device.DeviceTensor.from_numpy(q), device.DeviceTensor.from_numpy(wq),
+                         device.DeviceTensor.from_numpy(k), device.DeviceTensor.from_numpy(wk),
+                         device.DeviceTensor.from_numpy(v), device.DeviceTensor.from_numpy(pos),
+                         device.DeviceTensor.from_numpy(np.array([3, 10], np.int64)),
+                         device.DeviceTensor.empty((2, 4, 128), np.float32), kc, vc, eps=EPS, rope=abi.qwen3_rope())
+    device.synchronize()
+    with pytest.raises(ArclightError, match="out of range"):
+        fattn.device_errors()
+    fattn.device_errors()                                  # cleared
+    assert kc.numpy(np.uint16)[3].any() and vc.numpy(np.uint16)[3].any()
+    assert not np.delete(kc.numpy(np.uint16), 3, axis=0).any() and not np.delete(vc.numpy(np.uint16), 3, axis=0).any()
