@@ -30,7 +30,10 @@ def _case(name):
     print(f"\n[case] {name}", flush=True)
 
 
-def test_decode_loop_graph_replay(gpu):
+@pytest.mark.parametrize("one_launch_inputs", [False, True])
+def test_decode_loop_graph_replay(gpu, one_launch_inputs):
+    """one_launch_inputs: Q, K and V of a layer through al_attn_inputs_f32
+    instead of the three separate ops."""
     from arclight_amd import device, fattn, kv, matmul, prologue
     Hq, Hkv, D, L, N = 32, 8, 128, 2, 2560
     K = Hq * D
@@ -77,10 +80,14 @@ def test_decode_loop_graph_replay(gpu):
 
     def enqueue_step():
         for il in range(L):
-            prologue.rms_norm_rope(d_qc, d_wq[il], d_pos, eps=EPS, rope=rope, y=d_q[il], stream=stream)
-            prologue.rms_norm_rope(d_kc, d_wk[il], d_pos, eps=EPS, rope=rope, y=ring.cache_rows(il, "k"), rows=d_row,
-                                   stream=stream)
-            fattn.set_rows(ring.cache_rows(il, "v"), d_vc, d_row, stream=stream)
+            if one_launch_inputs:
+                prologue.attn_inputs(d_qc, d_wq[il], d_kc, d_wk[il], d_vc, d_pos, d_row, d_q[il],
+                                     ring.cache_rows(il, "k"), ring.cache_rows(il, "v"), eps=EPS, rope=rope, stream=stream)
+            else:
+                prologue.rms_norm_rope(d_qc, d_wq[il], d_pos, eps=EPS, rope=rope, y=d_q[il], stream=stream)
+                prologue.rms_norm_rope(d_kc, d_wk[il], d_pos, eps=EPS, rope=rope, y=ring.cache_rows(il, "k"),
+                                       rows=d_row, stream=stream)
+                fattn.set_rows(ring.cache_rows(il, "v"), d_vc, d_row, stream=stream)
             qv = device.DeviceTensor(d_q[il].buf, abi.AL_TYPE_F32, (1, 1, Hq, D), None, 0, abi.Q_AXES)
             fattn.flash_attn_ext(qv, ring.get_k(il, NKV), ring.get_v(il, NKV), scale=scale, dst=d_att[il],
                                  kv_len=NKV, causal_pos0=0, stream=stream, dyn_len=d_dyn)
@@ -91,7 +98,7 @@ def test_decode_loop_graph_replay(gpu):
     try:
         for s in range(STEPS):
             p = P0 + s
-            how = "eager" if s == 0 else "graph replay"
+            how = ("eager" if s == 0 else "graph replay") + (", one-launch inputs" if one_launch_inputs else "")
             _case(f"graph decode: step {s} at position {p} ({how})")
             rows, n_kv = ring.cells.place([(p, [0])])
             assert n_kv <= NKV and ring.cells.implicit([(p, [0])], n_kv) == (p + 1, p)
