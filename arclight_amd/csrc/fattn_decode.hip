@@ -237,7 +237,11 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             uint2 mk = {0, 0};
             if constexpr (HAS_MASK) mk = *(const uint2 *) (st + 8192 + 32 * n + 8 * g);
 
-            const bool full = !HAS_MASK && cs + kSC - 1 <= lim_min;
+            // a stage is taken whole when the length / causal limit passes it
+            // and, with a mask, every mask value of the stage is +0 (the
+            // masked arithmetic would add zeros)
+            bool full = cs + kSC - 1 <= lim_min;
+            if constexpr (HAS_MASK) full = full && __all((mk.x | mk.y) == 0u);
             bool vis_any[4] = {!!full, !!full, !!full, !!full};
             half4 pf[RB];
 #pragma unroll

@@ -73,9 +73,9 @@ class Layers:
             self.q.append(q); self.k.append(k); self.v.append(v); self.dst.append(d)
         device.synchronize()
 
-    def args(self, l, stream, scale, kv_len, causal_pos0=-1, q=None, dst=None):
+    def args(self, l, stream, scale, kv_len, causal_pos0=-1, q=None, dst=None, mask=None):
         from arclight_amd import fattn
-        return fattn.fattn_args(q or self.q[l], self.k[l], self.v[l], None, None, dst or self.dst[l],
+        return fattn.fattn_args(q or self.q[l], self.k[l], self.v[l], mask, None, dst or self.dst[l],
                                 scale=scale, kv_len=kv_len, causal_pos0=causal_pos0, stream=stream)
 
 
@@ -115,6 +115,18 @@ def time_graph(lib, stream, arg_list, steps, warmup, enqueue=None):
     return ms
 
 
+def causal_mask_f16(T, n_kv, pos0, kv_len):
+    """The f16 0 / -inf mask nnml builds for one sequence whose token t sits
+    at position pos0 + t over cells holding positions 0 .. kv_len - 1
+    (set_inputs_attn_mask, cgraph.cpp:1224-1261): PAD(T, 64) rows."""
+    rows = (T + 63) // 64 * 64
+    m = np.full((1, 1, rows, n_kv), -np.inf, dtype=np.float16)
+    c = np.arange(n_kv)
+    for t in range(T):
+        m[0, 0, t, (c < kv_len) & (c <= pos0 + t)] = 0.0
+    return m
+
+
 def decode_bytes(ctx, Hq, Hkv, D, T=1):
     return 2 * ctx * Hkv * D * 2 + 2 * T * Hq * D * 4
 
@@ -126,17 +138,24 @@ def prefill_flops(T_total, chunk, Hq, D):
     return 4 * D * Hq * pairs
 
 
-def bench_decode(lib, stream, a, ctx=None, L=None, Hq=32, T=1, steps=None):
+def bench_decode(lib, stream, a, ctx=None, L=None, Hq=32, T=1, steps=None, explicit_mask=False):
     """Decode (T = 1) or speculative verify (T drafts at positions ctx..ctx+T-1,
     causal among them) over L layers, each with its own cache slice of
-    PAD(ctx + T, 256) cells."""
+    PAD(ctx + T, 256) cells. explicit_mask: the f16 0 / -inf mask tensor
+    (PAD(T, 64) rows, as set_inputs_attn_mask builds it) instead of the
+    implicit length / causal description, i.e. the call as nnml makes it."""
     Hkv, D = 8, 128
     ctx = ctx or a.ctx
     L = L or a.layers
     scale = 1.0 / math.sqrt(D)
     n_kv = (ctx + T + 255) // 256 * 256 if T > 1 else ctx
     lay = Layers(L, T, Hq, Hkv, D, n_kv, a.seed)
-    if T == 1:
+    if explicit_mask:
+        from arclight_amd import fattn
+        m = fattn.upload_mask(causal_mask_f16(T, n_kv, ctx if T > 1 else ctx - 1, ctx + (T if T > 1 else 0)))
+        args = [lay.args(l, stream, scale, kv_len=0, mask=m) for l in range(L)]
+        byts = decode_bytes(ctx + (T if T > 1 else 0), Hq, Hkv, D, T)
+    elif T == 1:
         args = [lay.args(l, stream, scale, kv_len=ctx) for l in range(L)]
         byts = decode_bytes(ctx, Hq, Hkv, D)
     else:
@@ -196,6 +215,8 @@ def bench_other_configs(lib, stream, a):
                     "us_per_layer": round(r["kernel_ms_mean"] * 1e3, 2)})
         print(f"[bench] {out[-1]}", file=sys.stderr, flush=True)
 
+    dec("decode, Qwen3-4B shape, context 32768, 36 layers, explicit f16 mask (the call as nnml makes it, "
+        "no length hints)", ctx=32768, L=36, explicit_mask=True)
     dec("decode, Qwen3-4B shape, context 4096, 36 layers", ctx=4096, L=36)
     dec("decode, Qwen3-4B shape, context 16384, 36 layers", ctx=16384, L=36)
     dec("verify 4 drafts, Qwen3-8B shape, context 8192, 36 layers", ctx=8192, L=36, T=4)
