@@ -249,7 +249,18 @@ __device__ __forceinline__ bool score_tile(const Tile<RB> & cur, const int cb, c
 #pragma unroll
             for (int j = 0; j < 8; ++j) s[rb][j >> 2][j & 3] = p.softcap * tanhf(s[rb][j >> 2][j & 3]);
     }
-    const bool full = !HAS_MASK && cb + 31 <= lim_min;
+    // the tile is taken whole when the length / causal limit passes it and,
+    // with a mask, every mask value the wave holds is +0 (the masked
+    // arithmetic would add zeros)
+    bool full = cb + 31 <= lim_min;
+    if constexpr (HAS_MASK) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bits |= cur.mk[rb][i];
+        full = full && __all(bits == 0u);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) vis_any[j] = true;
     if (!full) {
