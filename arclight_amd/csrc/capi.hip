@@ -338,7 +338,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         dwaves = 2;
         stages = 3;
     }
-    // 17..32 rows (two row blocks) exist as 8 x 2 with implicit masks only
+    // 17..32 rows (two row blocks) exist as 8 x 2
     const bool two_blocks = p.R > 16;
     if (two_blocks) {
         dwaves = 8;
@@ -349,7 +349,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
                                      m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
     const int64_t decode_units = Hkv * B;
     const size_t decode_q_lds = two_blocks ? 16384 : 8192;                 // the query rows, f32
-    if ((p.R <= 16 || (p.R <= 32 && !m.data)) && prefer_decode() && (size_t) lds_per_block >= decode_lds + decode_q_lds &&
+    if (p.R <= 32 && prefer_decode() && (size_t) lds_per_block >= decode_lds + decode_q_lds &&
         mask_ok &&
         q_slice < INT32_MAX &&
         decode_units * sizeof(unsigned) <= kFattnCounterBytes &&

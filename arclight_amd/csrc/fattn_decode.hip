@@ -6,7 +6,7 @@
 // Work decomposition. A workgroup owns one kv head of one cell range (a
 // split) of one stream and keeps up to 16 query rows of the head's group
 // (row r -> token r / G, head kvh*G + r % G), or up to 32 as two MFMA row
-// blocks sharing every K/V operand read (speculative verify, implicit masks). Its WS wavefronts take the
+// blocks sharing every K/V operand read (speculative verify). Its WS wavefronts take the
 // range's 16-cell stages in turn (wave ws: stages ws, ws + WS, ...), each
 // with a private ring of NB LDS stage buffers, so the waves never wait for
 // each other until the end. The 1-D grid runs split fastest.
@@ -54,14 +54,14 @@ constexpr int kSC = 16;                                   // cells per stage
 template <int WS, int NB, bool HAS_MASK, int RB>
 __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p) {
     static_assert(WS == 2 || WS == 4 || WS == 8, "the wave merge is a binary tree");
-    static_assert(RB == 1 || (RB == 2 && !HAS_MASK), "32 rows with implicit masks only");
+    static_assert(RB == 1 || RB == 2, "16 or 32 rows");
     constexpr int PER = 8 + (HAS_MASK ? 1 : 0);           // DMA loads per stage
     constexpr int STAGE = 8192 + (HAS_MASK ? 1024 : 0);   // K rows, V rows, mask rows
     constexpr int REC = 16 * RB * kRowStride;             // floats of one state record (16 RB rows)
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
     __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
-    __shared__ int s_last;
+    int & s_last = *(int *) qlds;                         // after the prologue the query rows are dead
 
     const int lane = threadIdx.x & 63;
     const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -124,15 +124,15 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     }
 
     // Mask rows (f16, cells along a row) also travel by DMA, one 1 KiB block
-    // per stage: lane l < 32 loads cells 8(l & 1)..+7 of row l >> 1 to LDS
-    // bytes 16 l (lanes 32..63 repeat lanes 0..31), from a buffer over the
-    // stream's mask slice; cells past a row read whatever follows, and are
-    // past the length limit anyway.
+    // per stage: lane l loads cells 8(l & 1)..+7 of row l >> 1 to LDS bytes
+    // 16 l (with one row block, lanes 32..63 repeat lanes 0..31), from a
+    // buffer over the stream's mask slice; cells past a row read whatever
+    // follows, and are past the length limit anyway.
     int4v md = {0, 0, 0, 0};
     uint32_t msrc = 0;
     if constexpr (HAS_MASK) {
         md = raw_desc(p.mask + (int64_t) (b % p.m_ne3) * p.m_nb3, p.m_slice_bytes);
-        const int mrow = (lane >> 1) & 15;
+        const int mrow = (lane >> 1) & (16 * RB - 1);
         const int mt_ = mrow < rows_here ? mrow / p.G : 0;
         const int mh = kvh * p.G + (mrow < rows_here ? mrow % p.G : 0);
         msrc = (uint32_t) ((int64_t) mt_ * p.m_nb1 + (int64_t) (mh % p.m_ne2) * p.m_nb2) + (uint32_t) ((lane & 1) * 16);
@@ -234,14 +234,23 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             half4 vt[8];
 #pragma unroll
             for (int mb = 0; mb < 8; ++mb) vt[mb] = lds_read_tr16(st + vread + (((2 * mb + ((n & 3) >> 1)) ^ vcell) << 4));
-            uint2 mk = {0, 0};
-            if constexpr (HAS_MASK) mk = *(const uint2 *) (st + 8192 + 32 * n + 8 * g);
+            uint2 mk[RB];
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb) {
+                mk[rb] = uint2{0, 0};
+                if constexpr (HAS_MASK) mk[rb] = *(const uint2 *) (st + 8192 + 32 * (16 * rb + n) + 8 * g);
+            }
 
             // a stage is taken whole when the length / causal limit passes it
             // and, with a mask, every mask value of the stage is +0 (the
             // masked arithmetic would add zeros)
             bool full = cs + kSC - 1 <= lim_min;
-            if constexpr (HAS_MASK) full = full && __all((mk.x | mk.y) == 0u);
+            if constexpr (HAS_MASK) {
+                uint32_t bits = 0;
+#pragma unroll
+                for (int rb = 0; rb < RB; ++rb) bits |= mk[rb].x | mk[rb].y;
+                full = full && __all(bits == 0u);
+            }
             bool vis_any[4] = {!!full, !!full, !!full, !!full};
             half4 pf[RB];
 #pragma unroll
@@ -261,7 +270,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                         bool vis = cs + 4 * g + i <= lim[rb];
                         float x = sc[i];
                         if constexpr (HAS_MASK) {
-                            const uint32_t w = i < 2 ? mk.x : mk.y;
+                            const uint32_t w = i < 2 ? mk[rb].x : mk[rb].y;
                             const float mv = slope[rb] * f16_bits_to_float((uint16_t) (w >> (16 * (i & 1))));
                             vis = vis && (mv != -AL_INF);
                             x += mv;
@@ -498,10 +507,11 @@ size_t fattn_decode_lds_bytes(int waves, int stages, bool mask) {
 
 hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream) {
     if (p.R > 16) {
-        // 17..32 rows: two row blocks, implicit masks, 8 waves x 2 stages
-        if (p.R > 32 || p.mask || waves != 8 || stages != 2) return hipErrorInvalidValue;
+        // 17..32 rows: two row blocks, 8 waves x 2 stages
+        if (p.R > 32 || waves != 8 || stages != 2) return hipErrorInvalidValue;
         const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
-        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2>), grid, dim3(8 * 64), 0, stream, p);
+        if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, true, 2>), grid, dim3(8 * 64), 0, stream, p);
+        else        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2>), grid, dim3(8 * 64), 0, stream, p);
         return hipGetLastError();
     }
     switch (waves * 10 + stages) {

@@ -295,3 +295,18 @@ def test_decode_kernel_two_row_blocks(gpu):
     _check("two row blocks, 2 streams, 20 rows", q, k, v, scale=SCALE, kv_len=1493, causal_pos0=1488)
     q, k, v = O.make_inputs(63, T=3, Hq=56, Hkv=7, n_kv=700)
     _check("two row blocks, 24 rows, G 8", q, k, v, scale=SCALE, kv_len=650)
+
+
+def test_decode_kernel_two_row_blocks_explicit_mask(gpu):
+    # 17..32 rows per kv head with the f16 mask tensor: the masked
+    # two-row-block decode kernel, with the causal mask of 8 drafts, a mask
+    # broadcast over two streams with ALiBi biases in it, and mask stages
+    # that are all zero next to ones that are not
+    q, k, v = O.make_inputs(64, T=8, Hq=32, Hkv=8, n_kv=2304)
+    _check("two row blocks, explicit causal mask", q, k, v, O.causal_mask(8, 2304, 2048, kv_len=2056), scale=SCALE)
+    rng = np.random.default_rng(65)
+    q, k, v = O.make_inputs(65, B=2, T=6, Hq=16, Hkv=4, n_kv=1024)
+    m = O.causal_mask(6, 1024, 1000, kv_len=1006)
+    m[..., 200:260] = rng.uniform(-3, 0, (1, 1, m.shape[2], 60)).astype(np.float16)
+    m[..., 300] = -np.inf
+    _check("two row blocks, mask with biases, ALiBi, 2 streams", q, k, v, m, scale=SCALE, max_bias=8.0)
