@@ -70,3 +70,34 @@ def test_struct_layouts_match_c(tmp_path):
     assert got[0] == [ctypes.sizeof(T), T.ne.offset, T.nb.offset, T.data.offset]
     assert got[1] == [ctypes.sizeof(A), A.scale.offset, A.prec.offset, A.kv_len.offset, A.causal_pos0.offset,
                       A.stream.offset, A.workspace_bytes.offset]
+
+
+def test_attn_inputs_layout_matches_c(tmp_path):
+    """al_attn_inputs_args (arclight_prologue.h) against its ctypes mirror,
+    and al_fattn_args.dyn_len, the last field the graph-replay path adds."""
+    src = tmp_path / "probe2.c"
+    src.write_text(
+        '#include <stdio.h>\n#include <stddef.h>\n#include "arclight_prologue.h"\n'
+        "int main(void) {\n"
+        ' printf("%zu %zu %zu %zu %zu\\n", sizeof(al_attn_inputs_args), offsetof(al_attn_inputs_args, v),'
+        " offsetof(al_attn_inputs_args, v_cache), offsetof(al_attn_inputs_args, eps),"
+        " offsetof(al_attn_inputs_args, rope));\n"
+        ' printf("%zu %zu\\n", sizeof(al_fattn_args), offsetof(al_fattn_args, dyn_len));\n'
+        " return 0; }\n")
+    exe = tmp_path / "probe2"
+    subprocess.run(["gcc", "-std=c11", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    got = [list(map(int, line.split())) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                                     check=True).stdout.splitlines()]
+    I, A = abi.AlAttnInputsArgs, abi.AlFattnArgs
+    assert got[0] == [ctypes.sizeof(I), I.v.offset, I.v_cache.offset, I.eps.offset, I.rope.offset]
+    assert got[1] == [ctypes.sizeof(A), A.dyn_len.offset]
+
+
+def test_attn_inputs_rejects_missing_operands_without_gpu():
+    """Argument checks run before any device call: no arguments, and a Q
+    tensor of the wrong type, come back as AL_ERR_INVALID / UNSUPPORTED."""
+    from arclight_amd import _lib
+    lib = _lib.load()
+    assert lib.al_attn_inputs_f32(None, None) == abi.AL_ERR_INVALID
+    a = abi.AlAttnInputsArgs()                     # every tensor empty
+    assert lib.al_attn_inputs_f32(ctypes.byref(a), None) in (abi.AL_ERR_INVALID, abi.AL_ERR_UNSUPPORTED)
