@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -155,6 +156,11 @@ struct Plan {
     int rows_per_tile = 16;
     size_t counters_bytes = 0;
     size_t part_bytes = 0;
+    // split-KV plan of a many-row call with a mask tensor, gated behind the
+    // mask pass and the prefill kernel (FattnParams::row_lim)
+    bool masked_prefill = false;
+    int32_t prefill_tiles = 0;
+    size_t lims_bytes = 0;
 };
 
 bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
@@ -317,10 +323,10 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     // workgroup per 64-row tile, when that alone fills the device.
     const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
     // (it keeps the running max on scores as computed: needs scale > 0 unless softcapped)
-    if (!m.data && !p.dyn && p.R > 32 && prefill_tiles * Hkv * B >= n_cu &&
-        lds_per_block >= (int64_t) fattn_prefill_lds_bytes() &&
-        q_slice < INT32_MAX &&
-        (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill()) {
+    const bool prefill_shape = !p.dyn && p.R > 32 && prefill_tiles * Hkv * B >= n_cu &&
+                               lds_per_block >= (int64_t) fattn_prefill_lds_bytes() && q_slice < INT32_MAX &&
+                               (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill();
+    if (!m.data && prefill_shape) {
         pl.kernel = kPrefill;
         pl.rows_per_tile = kFattnPrefillRows;
         p.n_row_tiles = (int32_t) prefill_tiles;
@@ -409,6 +415,11 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         pl.counters_bytes = kFattnCounterBytes;
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
     }
+    if (m.data && prefill_shape) {
+        pl.masked_prefill = true;
+        pl.prefill_tiles = (int32_t) prefill_tiles;
+        pl.lims_bytes = ((size_t) T * p.m_ne2 * p.m_ne3 * sizeof(int32_t) + 255) / 256 * 256;
+    }
     *out = pl;
     return AL_OK;
 }
@@ -420,7 +431,7 @@ extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
     if (al_device_cu_count(&n_cu) != AL_OK || al_device_lds_per_block(&lds) != AL_OK) return 0;
     Plan pl;
     if (make_plan(a, n_cu, lds, &pl) != AL_OK) return 0;
-    return pl.counters_bytes + pl.part_bytes;
+    return pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
 }
 
 extern "C" int al_fattn_f16(const al_fattn_args * a) {
@@ -431,7 +442,8 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
     Plan pl;
     rc = make_plan(a, n_cu, lds, &pl);
     if (rc != AL_OK) return rc;
-    const size_t need = pl.counters_bytes + pl.part_bytes;
+    const size_t need = pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
+    int32_t * lims = nullptr;
     if (need) {
         void * ws = a->workspace;
         if (ws) {
@@ -444,10 +456,37 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
         }
         pl.p.counters = (unsigned *) ws;
         pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
+        lims = (int32_t *) ((char *) ws + pl.counters_bytes + pl.part_bytes);
     }
     rc = al_device_error_flag(&pl.p.err);
     if (rc != AL_OK) return rc;
     hipError_t e;
+    if (pl.masked_prefill) {
+        // the mask pass, then the prefill kernel on the mask's row limits and
+        // the split-KV kernel; the pass leaves exactly one of them running
+        static std::atomic<int> next_gen{0};
+        int gen = ++next_gen;
+        if (gen <= 0) {
+            next_gen = 1;
+            gen = 1;
+        }
+        int * gate = pl.p.err + 3;
+        hipStream_t st = (hipStream_t) a->stream;
+        FattnParams pp = pl.p;
+        pp.n_row_tiles = pl.prefill_tiles;
+        pp.n_split = 1;
+        pp.cells_per_split = 0;
+        pp.row_lim = lims;
+        pp.gate = gate;
+        pp.gen = gen;
+        e = fattn_mask_limits_launch(pl.p, lims, gate, gen, st);
+        if (e == hipSuccess) e = fattn_prefill_launch(pp, st);
+        pl.p.gate = gate;
+        pl.p.gen = gen;
+        if (e == hipSuccess) e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, st);
+        if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
+        return AL_OK;
+    }
     switch (pl.kernel) {
         case kPrefill: e = fattn_prefill_launch(pl.p, (hipStream_t) a->stream); break;
         case kDecode:  e = fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream); break;

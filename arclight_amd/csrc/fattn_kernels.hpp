@@ -35,6 +35,14 @@ struct FattnParams {
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
     int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
     const int32_t * dyn;            // decode kernel: device {kv_len, causal_pos0} read at run time, or null
+    // Many-row calls with a mask tensor: the mask pass writes each mask
+    // row's last visible cell to row_lim ([m_ne3][m_ne2][T]) and stores gen
+    // in *gate when some row is not a run of zeros followed by -inf; the
+    // prefill kernel then returns at once and the split-KV kernel, which
+    // otherwise returns at once, takes the call.
+    const int32_t * row_lim;
+    const int * gate;
+    int32_t gen;
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).
@@ -46,6 +54,7 @@ hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStr
 // Prefill kernel: 64-row tiles, implicit masks only, one workgroup per
 // (kv head, row tile, stream); needs fattn_prefill_lds_bytes() of LDS.
 hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream);
+hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, int gen, hipStream_t stream);
 size_t fattn_prefill_lds_bytes();
 constexpr int kFattnPrefillRows = 64;
 

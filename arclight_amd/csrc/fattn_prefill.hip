@@ -197,8 +197,24 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int row0 = rt * kPRows;
     const int rows_here = min(kPRows, p.R - row0);
     const int t_last = (row0 + rows_here - 1) / p.G;
+    // gated behind the mask pass: the split-KV kernel takes a rejected mask
+    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.gen) return;
     int hi = p.kv_hi;
     if (p.causal_pos0 >= 0) hi = (int) min((int64_t) hi, p.causal_pos0 + t_last + 1);
+    // with a mask tensor, each row's last visible cell from the mask pass;
+    // lane l takes row l of the tile, the workgroup's cells end after the
+    // largest of them
+    auto mask_lim = [&](const int rr) {
+        const int r = row0 + rr;
+        const int hq = kvh * p.G + r % p.G;
+        return p.row_lim[((int64_t) (b % p.m_ne3) * p.m_ne2 + hq % p.m_ne2) * p.T + r / p.G];
+    };
+    if (p.row_lim) {
+        int mx = mask_lim(min(lane, rows_here - 1));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
+        hi = __builtin_amdgcn_readfirstlane(min(hi, mx + 1));          // the same in every lane
+    }
 
     const char * kbase = p.k + (int64_t) (b / p.rk3) * p.k_nb3 + (int64_t) kvh * p.k_nb2;
     const char * vbase = p.v + (int64_t) (b / p.rv3) * p.v_nb3 + (int64_t) kvh * p.v_nb2;
@@ -268,7 +284,20 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     int lim[kPRB];
 #pragma unroll
     for (int rb = 0; rb < kPRB; ++rb) lim[rb] = row_limit(p, hi, rvalid[rb], tok[rb]);
-    const int lim_min = row_limit(p, hi, true, (row0 + min(32 * rh, rows_here - 1)) / p.G);   // this wave's first token
+    int lim_min = row_limit(p, hi, true, (row0 + min(32 * rh, rows_here - 1)) / p.G);   // this wave's first token
+    if (p.row_lim) {
+        // the mask's limits, within the length / causal ones; lim_min: the
+        // smallest over the wave's valid rows
+        int mn = INT32_MAX;
+#pragma unroll
+        for (int rb = 0; rb < kPRB; ++rb) {
+            if (rvalid[rb]) lim[rb] = min(lim[rb], mask_lim(32 * rh + 16 * rb + n));
+            mn = min(mn, rvalid[rb] ? lim[rb] : INT32_MAX);
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) mn = min(mn, __shfl_xor(mn, off));
+        lim_min = __builtin_amdgcn_readfirstlane(mn);
+    }
 
     // p = exp2(s * cexp - m * cexp); the max is tracked on s as computed
     // (raw dot products, or softcapped scores in natural units)
@@ -440,7 +469,52 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     }
 }
 
+// One workgroup per mask row (token t of mask slice (i2, i3)) over cells
+// [0, n_kv): the last cell holding +-0 (-1 if none) into lims, and gen into
+// *gate when the row is not a run of zeros followed by -inf (another value,
+// or a zero after a -inf).
+__global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, int32_t * lims, int * gate, const int gen) {
+    const int t = blockIdx.x, i2 = blockIdx.y, i3 = blockIdx.z;
+    const uint16_t * row = (const uint16_t *) (p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3);
+    int last0 = -1, first_inf = INT32_MAX, bad = 0;
+    for (int c = threadIdx.x; c < p.n_kv; c += blockDim.x) {
+        const uint16_t h = row[c];
+        if ((h & 0x7fffu) == 0) last0 = c;
+        else if (h == 0xfc00u) first_inf = min(first_inf, c);
+        else bad = 1;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        last0 = max(last0, __shfl_xor(last0, off));
+        first_inf = min(first_inf, __shfl_xor(first_inf, off));
+        bad |= __shfl_xor(bad, off);
+    }
+    __shared__ int s[3][4];
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        s[0][w] = last0;
+        s[1][w] = first_inf;
+        s[2][w] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < (int) (blockDim.x >> 6); ++i) {
+            last0 = max(last0, s[0][i]);
+            first_inf = min(first_inf, s[1][i]);
+            bad |= s[2][i];
+        }
+        lims[((int64_t) i3 * p.m_ne2 + i2) * p.T + t] = last0;
+        if (bad || last0 > first_inf) __hip_atomic_exchange(gate, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 }  // namespace
+
+hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, int gen, hipStream_t stream) {
+    const dim3 grid((unsigned) p.T, (unsigned) p.m_ne2, (unsigned) p.m_ne3);
+    hipLaunchKernelGGL(mask_limits_kernel, grid, dim3(256), 0, stream, p, lims, gate, gen);
+    return hipGetLastError();
+}
 
 size_t fattn_prefill_lds_bytes() { return (size_t) kLds; }
 

@@ -38,6 +38,8 @@ using namespace fattn;
 
 template <int RB, int W, bool PREFETCH, bool HAS_MASK>
 __global__ __launch_bounds__(W * 64) void fattn_splitkv_kernel(const FattnParams p) {
+    // gated behind the prefill kernel: only when the mask pass rejected the mask
+    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p.gen) return;
     constexpr int ROWS = 16 * RB;
     // LDS records of the wave merge: a tree when W/2 records fit in 40 KiB,
     // else one record that wave 0 merges the others through in turn

@@ -88,3 +88,23 @@ def test_prefill_chunks_equal_one_causal_call(gpu):
         qc = np.ascontiguousarray(q[:, 512 * c:512 * (c + 1)])
         got = run_gpu(qc, k, v, scale=SCALE, kv_len=512 * (c + 1), causal_pos0=512 * c)
         assert_parity(got, whole[:, 512 * c:512 * (c + 1)], what=f"chunk {c} vs one call")
+
+
+def test_prefill_explicit_mask_on_the_prefill_kernel(gpu):
+    # a 512-token causal chunk with the f16 mask tensor and no length hints:
+    # a mask of zero runs then -inf goes to the prefill kernel on the mask's
+    # row limits; a mask with a hole and biases goes to the split-KV kernel;
+    # and a plain mask again after that (the gate holds the last call's tag)
+    n_kv = 2048
+    q, k, v = O.make_inputs(4096, T=512, Hq=32, Hkv=8, n_kv=n_kv)
+    m = O.causal_mask(512, n_kv, 1536, kv_len=2000)
+    _case("prefill chunk 512, explicit causal + length mask")
+    assert_parity(run_gpu(q, k, v, m, scale=SCALE), O.attention(q, k, v, m, scale=SCALE), what="explicit causal mask")
+    m2 = m.copy()
+    m2[..., 100] = -np.inf
+    m2[..., 200:210] = np.float16(-1.5)
+    _case("prefill chunk 512, mask with a hole and biases")
+    assert_parity(run_gpu(q, k, v, m2, scale=SCALE), O.attention(q, k, v, m2, scale=SCALE), what="mask with hole")
+    m3 = O.causal_mask(512, n_kv, 0, kv_len=512)
+    _case("prefill first chunk, explicit causal mask")
+    assert_parity(run_gpu(q, k, v, m3, scale=SCALE), O.attention(q, k, v, m3, scale=SCALE), what="first chunk mask")
