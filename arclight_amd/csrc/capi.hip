@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -46,12 +47,17 @@ void al_clear_error() { g_last_error.clear(); }
 
 namespace {
 
+// Library-owned split-KV workspace of one stream.
+struct Workspace {
+    void * ptr = nullptr;
+    size_t bytes = 0;
+};
+
 struct DeviceState {
     bool       init = false;
     int        n_cu = 0;
     int        lds_per_block = 0;
-    void *     ws = nullptr;        // library-owned split-KV workspace
-    size_t     ws_bytes = 0;
+    std::map<void *, Workspace> ws;     // per stream (nullptr: the default stream)
     int *      err = nullptr;       // kernel-recorded errors (set_rows)
 };
 
@@ -110,33 +116,36 @@ int al_device_lds_per_block(int * bytes) {
     return AL_OK;
 }
 
-// Library-owned workspace, zero-filled when (re)allocated. The kernels leave
-// the counter region zeroed after every call.
-static int library_workspace(size_t bytes, void ** ptr) {
+// Library-owned workspace of (current device, stream), zero-filled when
+// (re)allocated. The kernels leave the counter region zeroed after every
+// call. One workspace per stream: calls on one stream are ordered, so they
+// can share counters and records; calls on different streams never do.
+static int library_workspace(size_t bytes, void * stream, void ** ptr) {
     int dev;
     DeviceState * st;
     const int rc = device_state(&dev, &st);
     if (rc != AL_OK) return rc;
     std::lock_guard<std::mutex> lk(g_mu);
-    if (st->ws_bytes < bytes) {
-        if (st->ws) {
-            hipError_t e = hipDeviceSynchronize();
+    Workspace & w = st->ws[stream];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            hipError_t e = hipDeviceSynchronize();   // also graphs replayed from a capture on this stream
             if (e != hipSuccess) return al_hip_fail(e, "hipDeviceSynchronize");
-            e = hipFree(st->ws);
+            e = hipFree(w.ptr);
             if (e != hipSuccess) return al_hip_fail(e, "hipFree(workspace)");
-            st->ws = nullptr;
-            st->ws_bytes = 0;
+            w.ptr = nullptr;
+            w.bytes = 0;
         }
         const size_t sz = std::max(bytes, (size_t) 4 << 20);
-        hipError_t e = hipMalloc(&st->ws, sz);
+        hipError_t e = hipMalloc(&w.ptr, sz);
         if (e != hipSuccess) return al_fail(AL_ERR_HIP, "hipMalloc(workspace %zu bytes): %s", sz, hipGetErrorString(e));
-        e = hipMemset(st->ws, 0, sz);
+        e = hipMemset(w.ptr, 0, sz);
         if (e != hipSuccess) return al_hip_fail(e, "hipMemset(workspace)");
-        e = hipDeviceSynchronize();               // zeroed before any stream's kernel uses it
+        e = hipDeviceSynchronize();               // zeroed before the stream's kernels use it
         if (e != hipSuccess) return al_hip_fail(e, "hipDeviceSynchronize");
-        st->ws_bytes = sz;
+        w.bytes = sz;
     }
-    *ptr = st->ws;
+    *ptr = w.ptr;
     return AL_OK;
 }
 
@@ -358,7 +367,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     if (p.R <= 32 && prefer_decode() && (size_t) lds_per_block >= decode_lds + decode_q_lds &&
         mask_ok &&
         q_slice < INT32_MAX &&
-        decode_units * sizeof(unsigned) <= kFattnCounterBytes &&
+        decode_units <= kFattnGateWord &&
         (uint64_t) (n_kv + 16) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
         (uint64_t) (n_kv + 16) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX) {
         pl.kernel = kDecode;
@@ -408,7 +417,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     int64_t cps_tiles = std::max<int64_t>(1, (tiles + n_split - 1) / n_split);
     p.cells_per_split = (int32_t) (cps_tiles * 32);
     n_split = std::max<int64_t>(1, (extent + p.cells_per_split - 1) / p.cells_per_split);
-    if ((size_t) units * sizeof(unsigned) > kFattnCounterBytes) n_split = 1;
+    if (units > kFattnGateWord) n_split = 1;
     if (n_split == 1) p.cells_per_split = (int32_t) std::max<int64_t>(32, (extent + 31) / 32 * 32);
     p.n_split = (int32_t) n_split;
     if (p.n_split > 1) {
@@ -416,8 +425,11 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
     }
     if (m.data && prefill_shape) {
+        // the gate lives in the counter region, which is reserved also when
+        // the split-KV plan has a single split
         pl.masked_prefill = true;
         pl.prefill_tiles = (int32_t) prefill_tiles;
+        pl.counters_bytes = kFattnCounterBytes;
         pl.lims_bytes = ((size_t) T * p.m_ne2 * p.m_ne3 * sizeof(int32_t) + 255) / 256 * 256;
     }
     *out = pl;
@@ -451,7 +463,7 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
                 return al_fail(AL_ERR_WORKSPACE, "fattn: workspace %llu bytes < %zu needed",
                                (unsigned long long) a->workspace_bytes, need);
         } else {
-            rc = library_workspace(need, &ws);
+            rc = library_workspace(need, a->stream, &ws);
             if (rc != AL_OK) return rc;
         }
         pl.p.counters = (unsigned *) ws;
@@ -463,14 +475,9 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
     hipError_t e;
     if (pl.masked_prefill) {
         // the mask pass, then the prefill kernel on the mask's row limits and
-        // the split-KV kernel; the pass leaves exactly one of them running
-        static std::atomic<int> next_gen{0};
-        int gen = ++next_gen;
-        if (gen <= 0) {
-            next_gen = 1;
-            gen = 1;
-        }
-        int * gate = pl.p.err + 3;
+        // the split-KV kernel; the pass leaves exactly one of them running,
+        // and the split-KV kernel clears the gate for the next call
+        int * gate = (int *) pl.p.counters + kFattnGateWord;
         hipStream_t st = (hipStream_t) a->stream;
         FattnParams pp = pl.p;
         pp.n_row_tiles = pl.prefill_tiles;
@@ -478,11 +485,9 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
         pp.cells_per_split = 0;
         pp.row_lim = lims;
         pp.gate = gate;
-        pp.gen = gen;
-        e = fattn_mask_limits_launch(pl.p, lims, gate, gen, st);
+        e = fattn_mask_limits_launch(pl.p, lims, gate, st);
         if (e == hipSuccess) e = fattn_prefill_launch(pp, st);
         pl.p.gate = gate;
-        pl.p.gen = gen;
         if (e == hipSuccess) e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, st);
         if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
         return AL_OK;

@@ -410,7 +410,6 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     constexpr int kItems = RB == 1 ? 2 : 1;                            // items per thread and round (registers)
     constexpr int kPairs = (16 * RB * kMaxSplit + WS * 64 - 1) / (WS * 64);
     float2 * ml_s = (float2 *) &lds[0][0][0];                          // [row][kMaxSplit]; the rings are free
-    const int n_pairs = rows_here * kMaxSplit;
     // (loads are unconditional, from clamped in-range addresses, and the
     // unused ones are replaced afterwards: no branch, so the O loads below
     // stay in flight while the pairs are stored)

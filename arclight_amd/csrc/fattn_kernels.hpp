@@ -36,13 +36,14 @@ struct FattnParams {
     int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
     const int32_t * dyn;            // decode kernel: device {kv_len, causal_pos0} read at run time, or null
     // Many-row calls with a mask tensor: the mask pass writes each mask
-    // row's last visible cell to row_lim ([m_ne3][m_ne2][T]) and stores gen
-    // in *gate when some row is not a run of zeros followed by -inf; the
+    // row's last visible cell to row_lim ([m_ne3][m_ne2][T]) and sets
+    // gate[0] when some row is not a run of zeros followed by -inf; the
     // prefill kernel then returns at once and the split-KV kernel, which
-    // otherwise returns at once, takes the call.
+    // otherwise returns at once, takes the call. gate[1] counts the split-KV
+    // workgroups that have read gate[0]; the last one clears both, so each
+    // call starts from a clear gate (also on a replayed graph).
     const int32_t * row_lim;
-    const int * gate;
-    int32_t gen;
+    int * gate;
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).
@@ -51,10 +52,12 @@ int fattn_splitkv_rows_per_tile(int R);
 int fattn_splitkv_waves(int rows_per_tile);
 hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
 
-// Prefill kernel: 64-row tiles, implicit masks only, one workgroup per
-// (kv head, row tile, stream); needs fattn_prefill_lds_bytes() of LDS.
+// Prefill kernel: 64-row tiles, one workgroup per (kv head, row tile,
+// stream); needs fattn_prefill_lds_bytes() of LDS. Masking is the implicit
+// length / causal rule, optionally narrowed per row by the row limits that
+// the mask pass (fattn_mask_limits_launch) derives from a mask tensor.
 hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream);
-hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, int gen, hipStream_t stream);
+hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream);
 size_t fattn_prefill_lds_bytes();
 constexpr int kFattnPrefillRows = 64;
 
@@ -73,5 +76,8 @@ constexpr int kFattnRecordStride = 132;
 constexpr int kFattnMaxSplit = 32;
 // Every workspace starts with a fixed arrival-counter region, so that no
 // call's merge records ever overlap another call's counters; kernels leave
-// it zeroed. Records follow it.
+// it zeroed. Its last two words are the gate of masked many-row calls
+// (FattnParams::gate), so at most kFattnGateWord counters precede them.
+// Records follow the region, then a masked call's row limits.
 constexpr size_t kFattnCounterBytes = 256u << 10;
+constexpr int kFattnGateWord = (int) (kFattnCounterBytes / 4) - 2;

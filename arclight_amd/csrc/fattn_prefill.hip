@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
     const int rows_here = min(kPRows, p.R - row0);
     const int t_last = (row0 + rows_here - 1) / p.G;
     // gated behind the mask pass: the split-KV kernel takes a rejected mask
-    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.gen) return;
+    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
     int hi = p.kv_hi;
     if (p.causal_pos0 >= 0) hi = (int) min((int64_t) hi, p.causal_pos0 + t_last + 1);
     // with a mask tensor, each row's last visible cell from the mask pass;
@@ -470,10 +470,10 @@ __global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnPara
 }
 
 // One workgroup per mask row (token t of mask slice (i2, i3)) over cells
-// [0, n_kv): the last cell holding +-0 (-1 if none) into lims, and gen into
-// *gate when the row is not a run of zeros followed by -inf (another value,
-// or a zero after a -inf).
-__global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, int32_t * lims, int * gate, const int gen) {
+// [0, n_kv): the last cell holding +-0 (-1 if none) into lims, and 1 into
+// gate[0] when the row is not a run of zeros followed by -inf (another
+// value, or a zero after a -inf).
+__global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, int32_t * lims, int * gate) {
     const int t = blockIdx.x, i2 = blockIdx.y, i3 = blockIdx.z;
     const uint16_t * row = (const uint16_t *) (p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3);
     int last0 = -1, first_inf = INT32_MAX, bad = 0;
@@ -504,15 +504,15 @@ __global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, i
             bad |= s[2][i];
         }
         lims[((int64_t) i3 * p.m_ne2 + i2) * p.T + t] = last0;
-        if (bad || last0 > first_inf) __hip_atomic_exchange(gate, gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (bad || last0 > first_inf) __hip_atomic_store(gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
 }  // namespace
 
-hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, int gen, hipStream_t stream) {
+hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream) {
     const dim3 grid((unsigned) p.T, (unsigned) p.m_ne2, (unsigned) p.m_ne3);
-    hipLaunchKernelGGL(mask_limits_kernel, grid, dim3(256), 0, stream, p, lims, gate, gen);
+    hipLaunchKernelGGL(mask_limits_kernel, grid, dim3(256), 0, stream, p, lims, gate);
     return hipGetLastError();
 }
 

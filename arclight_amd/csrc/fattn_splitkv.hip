@@ -38,14 +38,31 @@ using namespace fattn;
 
 template <int RB, int W, bool PREFETCH, bool HAS_MASK>
 __global__ __launch_bounds__(W * 64) void fattn_splitkv_kernel(const FattnParams p) {
-    // gated behind the prefill kernel: only when the mask pass rejected the mask
-    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != p.gen) return;
     constexpr int ROWS = 16 * RB;
     // LDS records of the wave merge: a tree when W/2 records fit in 40 KiB,
     // else one record that wave 0 merges the others through in turn
     constexpr int NSLOT = ((W / 2) * ROWS * kRowStride * 4 <= 40960) ? W / 2 : 1;
     __shared__ float lds[NSLOT * ROWS * kRowStride];
     __shared__ int s_last;
+
+    // Gated behind the prefill kernel: only when the mask pass rejected the
+    // mask. Each workgroup reads the gate (acquire: the load completes before
+    // the arrival below), then arrives; the last to arrive clears the gate
+    // and the arrival count for the next call in stream order.
+    if (p.gate) {
+        if (threadIdx.x == 0) {
+            const int gv = __hip_atomic_load(p.gate, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+            unsigned * arrived = (unsigned *) (p.gate + 1);
+            if (add_agent(arrived, 1u) == gridDim.x - 1) {
+                st_agent_u32(arrived, 0u);
+                __hip_atomic_store(p.gate, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            s_last = gv;
+        }
+        __syncthreads();
+        if (s_last == 0) return;
+        __syncthreads();                                          // s_last is reused below
+    }
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;

@@ -359,29 +359,56 @@ def bench_copy(stream, nbytes=1 << 30):
 
 
 def cpu_baseline(a):
-    """Oracle O2 (f32 restatement of arm.cpp:2196-2433) on host cores,
-    decode at the same shape on a bounded sample of layers."""
+    """Oracle O2 (f32 restatement of arm.cpp:2196-2433) on the host's cores:
+    one worker thread pinned to each physical core of the job's CPU share,
+    rows split over the workers as arm.cpp:2250-2257 does. Two bounded
+    samples of the benchmark's own workloads: 32K decode at the Qwen3-4B shape
+    (single-layer calls, GB/s) and the 2048-token prefill in 4 causal chunks
+    of 512 (one layer per repetition, TFLOP/s)."""
     from oracle import oracle as O
-    threads = min(16, os.cpu_count() or 1)
+    topo = O.cpu_topology()
+    cpus = topo["cpus"]
     Hq, Hkv, D, ctx = 32, 8, 128, a.ctx
+    scale = 1.0 / math.sqrt(D)
+
     n_layers = 2
     data = [O.make_inputs(a.seed + l, T=1, Hq=Hq, Hkv=Hkv, D=D, n_kv=ctx) for l in range(n_layers)]
-    scale = 1.0 / math.sqrt(D)
-    O.attention(*data[0], scale=scale, kv_len=ctx, threads=threads)     # warm
+    O.attention_pinned(*data[0], scale=scale, kv_len=ctx, cpus=cpus)     # warm
     t0 = time.perf_counter()
     calls = 0
     while True:
         for q, k, v in data:
-            O.attention(q, k, v, scale=scale, kv_len=ctx, threads=threads)
+            O.attention_pinned(q, k, v, scale=scale, kv_len=ctx, cpus=cpus)
             calls += 1
         el = time.perf_counter() - t0
         if el >= a.cpu_seconds or calls >= 400:
             break
     per = el / calls
     byts = decode_bytes(ctx, Hq, Hkv, D)
-    return {"value": byts / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+
+    T_total, chunk = 2048, 512
+    q, k, v = O.make_inputs(a.seed + 1, T=T_total, Hq=Hq, Hkv=Hkv, D=D, n_kv=T_total)
+    chunks = [np.ascontiguousarray(q[:, c * chunk:(c + 1) * chunk]) for c in range(T_total // chunk)]
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        for c, qc in enumerate(chunks):
+            O.attention_pinned(qc, k, v, scale=scale, kv_len=chunk * (c + 1), causal_pos0=chunk * c, cpus=cpus)
+        reps += 1
+        pel = time.perf_counter() - t0
+        if pel >= a.cpu_seconds or reps >= 20:
+            break
+    fl = prefill_flops(T_total, chunk, Hq, D)
+    where = (f"{len(cpus)} threads pinned one per physical core; host {topo['model']}, "
+             f"{topo['host_physical_cores']} physical cores, job share {topo['job_share']} CPUs "
+             f"(affinity {topo['allowed_cpus']}, cgroup quota {topo['cpu_quota']})")
+    return {"value": byts / per / 1e9, "unit": "GB/s", "cores": len(cpus), "kind": "port",
             "sample": f"decode ctx {ctx}, {calls} single-layer calls over {n_layers} distinct layers, "
-                      f"{el:.1f} s, {per * 1e3:.1f} ms/layer"}
+                      f"{el:.1f} s, {per * 1e3:.1f} ms/layer; {where}",
+            "cpu_model": topo["model"], "host_physical_cores": topo["host_physical_cores"], "pinned": True,
+            "prefill": {"value": fl * reps / pel / 1e12, "unit": "TFLOP/s",
+                        "sample": f"2048-token causal prefill in 4 chunks of 512, one layer per repetition, "
+                                  f"{reps} repetitions, {pel:.1f} s, {pel / reps * 1e3:.0f} ms/layer"}}
 
 
 def load_traffic(kernel, ctx):

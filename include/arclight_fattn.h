@@ -91,10 +91,16 @@ typedef struct al_tensor {
  * explicit mask alone, while wholly masked tiles are skipped unread.
  *
  * workspace: device scratch for split-KV partials. NULL lets the library use
- * its own per-device buffer (allocated on first use, grown when needed).
- * A caller workspace must be zero-filled before its first use: its first
- * 256 KiB hold arrival counters that every call leaves at zero again, the
- * rest holds per-call merge records. Calls that share one workspace must be
+ * its own buffer for the current device and args->stream (allocated on first
+ * use, grown when needed; a graph captured on a stream uses that stream's).
+ * A caller workspace must be zero-filled before its first use. Its first
+ * 256 KiB hold arrival counters; the last two words of that region gate a
+ * many-row call that carries a mask tensor. Every call leaves the region at
+ * zero again. Per-call merge records follow it, then (for a many-row call
+ * with a mask tensor) the row limits that a pass over the mask writes: the
+ * last visible cell of each mask row, which the prefill kernel reads when
+ * every row is a run of zeros followed by -inf; otherwise the gate sends
+ * the call to the general kernel. Calls that share one workspace must be
  * ordered on one stream.
  *
  * dyn_len: for a call captured once into a HIP graph and replayed for every

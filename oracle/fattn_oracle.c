@@ -28,10 +28,12 @@
  * from the ALiBi paper's construction), permutation invariance and
  * chunked-equals-one-shot causal prefill.
  */
+#define _GNU_SOURCE 1
 #include "fattn_oracle.h"
 
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -371,21 +373,49 @@ static void * worker(void * p) {
     return NULL;
 }
 
-static int run(const al_fattn_args * a, int n_threads, int mode) {
+/* The reference's worker pool (nnml/src/scheduler.cpp:122-146): nth threads,
+ * each running the op with its own ith. With cpus, thread i runs pinned to
+ * logical CPU cpus[i] (thread 0 is the caller, pinned for the call only). */
+static int run_on(const al_fattn_args * a, int n_threads, int mode, const int * cpus) {
     job_t j;
     const int rc = prepare(&j, a, n_threads, mode);
     if (rc != AL_OK) return rc;
     pthread_t * th = (pthread_t *) malloc(sizeof(pthread_t) * (size_t) j.nth);
     worker_t * ws = (worker_t *) malloc(sizeof(worker_t) * (size_t) j.nth);
     for (int i = 0; i < j.nth; ++i) { ws[i].j = &j; ws[i].ith = i; }
-    for (int i = 1; i < j.nth; ++i) pthread_create(&th[i], NULL, worker, &ws[i]);
+    cpu_set_t saved;
+    int restore = 0;
+    for (int i = 1; i < j.nth; ++i) {
+        pthread_attr_t at;
+        pthread_attr_init(&at);
+        if (cpus) {
+            cpu_set_t cs;
+            CPU_ZERO(&cs);
+            CPU_SET(cpus[i], &cs);
+            pthread_attr_setaffinity_np(&at, sizeof(cs), &cs);
+        }
+        pthread_create(&th[i], &at, worker, &ws[i]);
+        pthread_attr_destroy(&at);
+    }
+    if (cpus && pthread_getaffinity_np(pthread_self(), sizeof(saved), &saved) == 0) {
+        cpu_set_t cs;
+        CPU_ZERO(&cs);
+        CPU_SET(cpus[0], &cs);
+        restore = pthread_setaffinity_np(pthread_self(), sizeof(cs), &cs) == 0;
+    }
     worker(&ws[0]);
     for (int i = 1; i < j.nth; ++i) pthread_join(th[i], NULL);
+    if (restore) pthread_setaffinity_np(pthread_self(), sizeof(saved), &saved);
     free(th); free(ws);
     return AL_OK;
 }
 
+static int run(const al_fattn_args * a, int n_threads, int mode) { return run_on(a, n_threads, mode, NULL); }
+
 int orc_fattn_o2(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 2); }
+int orc_fattn_o2_pinned(const al_fattn_args * a, int n_threads, const int * cpus) {
+    return run_on(a, n_threads, 2, cpus);
+}
 int orc_fattn_o1(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 1); }
 int orc_fattn_o3(const al_fattn_args * a, int n_threads) { return run(a, n_threads, 3); }
 

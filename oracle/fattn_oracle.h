@@ -40,6 +40,8 @@ void     orc_f16_to_f32_n(const uint16_t * x, float * y, int64_t n);
 
 /* Attention oracles; return 0 or a negative al status. n_threads >= 1. */
 int orc_fattn_o2(const al_fattn_args * a, int n_threads);
+/* O2 with thread i pinned to logical CPU cpus[i] (the timed CPU baseline). */
+int orc_fattn_o2_pinned(const al_fattn_args * a, int n_threads, const int * cpus);
 int orc_fattn_o1(const al_fattn_args * a, int n_threads);
 int orc_fattn_o3(const al_fattn_args * a, int n_threads);
 

@@ -43,6 +43,8 @@ def lib():
             f = getattr(L, name)
             f.restype = ctypes.c_int
             f.argtypes = [ctypes.POINTER(abi.AlFattnArgs), ctypes.c_int]
+        L.orc_fattn_o2_pinned.restype = ctypes.c_int
+        L.orc_fattn_o2_pinned.argtypes = [ctypes.POINTER(abi.AlFattnArgs), ctypes.c_int, ctypes.c_void_p]
         L.orc_set_rows_f32_f16.restype = ctypes.c_int
         L.orc_set_rows_f32_f16.argtypes = [ctypes.POINTER(abi.AlTensor)] * 3
         L.orc_rms_norm_rope_f32.restype = ctypes.c_int
@@ -84,6 +86,68 @@ def _bits(a):
 def default_threads():
     n = os.cpu_count() or 1
     return max(1, min(n, 16))
+
+
+def _read(path):
+    try:
+        with open(path) as f:
+            return f.read().strip()
+    except OSError:
+        return None
+
+
+def cpu_topology():
+    """The host CPUs this process may run on, one logical CPU per physical
+    core: {"model", "host_physical_cores", "allowed_cpus", "cpu_quota",
+    "job_share", "cpus"}. `cpus` lists one logical CPU of each physical core
+    (socket, core id) in the affinity set, at most `job_share` of them: the
+    CPU share the job is given (the cgroup CPU quota, or OMP_NUM_THREADS when
+    the launcher sets it as the share), else every physical core."""
+    allowed = sorted(os.sched_getaffinity(0))
+    model = None
+    txt = _read("/proc/cpuinfo") or ""
+    for line in txt.splitlines():
+        if line.startswith("model name"):
+            model = line.split(":", 1)[1].strip()
+            break
+    cores, host_cores = {}, set()
+    for c in range(os.cpu_count() or 0):
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        pkg, core = _read(base + "physical_package_id"), _read(base + "core_id")
+        key = (int(pkg) if pkg is not None else 0, int(core) if core is not None else c)
+        host_cores.add(key)
+        if c in allowed and key not in cores:
+            cores[key] = c
+    quota = None
+    cm = _read("/sys/fs/cgroup/cpu.max")
+    if cm and not cm.startswith("max"):
+        q, per = cm.split()[:2]
+        quota = int(q) / int(per)
+    share = len(cores)
+    if quota:
+        share = min(share, max(1, int(quota)))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        share = min(share, int(omp))
+    cpus = [cores[k] for k in sorted(cores, key=lambda k: cores[k])][:share]
+    return {"model": model, "host_physical_cores": len(host_cores), "allowed_cpus": len(allowed),
+            "cpu_quota": quota, "job_share": share, "cpus": cpus}
+
+
+def attention_pinned(q, k, v, mask=None, *, scale, cpus, kv_len=0, causal_pos0=-1):
+    """O2 with one worker thread pinned to each logical CPU of `cpus` (the
+    reference's row split over that many workers); returns dst."""
+    k, v = _bits(k), _bits(v)
+    if mask is not None:
+        mask = _bits(mask)
+    B, T, Hq, _ = q.shape
+    dst = np.full((B, T, Hq, v.shape[3]), np.nan, dtype=np.float32)
+    a = build_args(q, k, v, mask, None, dst, scale=scale, kv_len=kv_len, causal_pos0=causal_pos0)
+    c = (ctypes.c_int * len(cpus))(*cpus)
+    rc = lib().orc_fattn_o2_pinned(ctypes.byref(a), len(cpus), ctypes.cast(c, ctypes.c_void_p))
+    if rc != 0:
+        raise RuntimeError(f"oracle O2 failed: {rc}")
+    return dst
 
 
 def build_args(q, k, v, mask=None, sinks=None, dst=None, *, scale, max_bias=0.0,

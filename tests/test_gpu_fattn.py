@@ -39,7 +39,7 @@ def test_decode_qwen3_4b_c512(gpu, explicit):
         _check("decode c512 implicit", q, k, v, scale=SCALE, kv_len=513)
 
 
-@pytest.mark.parametrize("ctx", [4096, 32768])
+@pytest.mark.parametrize("ctx", [4096, 16384, 32768])
 def test_decode_qwen3_4b_long(gpu, ctx):
     q, k, v = O.make_inputs(ctx, T=1, Hq=32, Hkv=8, n_kv=ctx)
     _check(f"decode ctx {ctx}", q, k, v, scale=SCALE, kv_len=ctx)

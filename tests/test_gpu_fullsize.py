@@ -62,9 +62,9 @@ def test_decode_qwen3_32b_ctx32768(gpu):
     assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=32768), ref, what="decode 32B ctx 32768")
 
 
-@pytest.mark.parametrize("pos0", [0, 3072])
+@pytest.mark.parametrize("pos0", [0, 1024, 2048, 3072])
 def test_prefill_qwen3_32b_chunk1024(gpu, pos0):
-    # first and last 1024-token chunk of a 4096-token prompt at 64 query heads
+    # the four 1024-token chunks of a 4096-token prompt at 64 query heads
     T, kv_len = 1024, pos0 + 1024
     q, k, v = O.make_inputs(1024 + pos0, T=T, Hq=64, Hkv=8, n_kv=kv_len)
     _case(f"prefill Qwen3-32B shape chunk 1024 pos0 {pos0}")
@@ -94,7 +94,7 @@ def test_prefill_explicit_mask_on_the_prefill_kernel(gpu):
     # a 512-token causal chunk with the f16 mask tensor and no length hints:
     # a mask of zero runs then -inf goes to the prefill kernel on the mask's
     # row limits; a mask with a hole and biases goes to the split-KV kernel;
-    # and a plain mask again after that (the gate holds the last call's tag)
+    # and a plain mask again after that (each call clears the gate it used)
     n_kv = 2048
     q, k, v = O.make_inputs(4096, T=512, Hq=32, Hkv=8, n_kv=n_kv)
     m = O.causal_mask(512, n_kv, 1536, kv_len=2000)

@@ -1,0 +1,146 @@
+"""Workspace and gate state across calls.
+
+- A many-row call with a mask tensor whose split-KV fallback plans a single
+  split (Qwen3-32B shape, 1024-token chunk: 128 row tiles x 8 kv heads fill
+  the device) still keeps its row limits out of the arrival-counter region:
+  a multi-split decode call that follows on the same library workspace
+  matches the oracle.
+- Masked many-row calls on two streams, one mask accepted by the mask pass
+  and one rejected, overlap without touching each other's gate or records.
+- A captured masked call replayed first with a rejected mask and then with
+  an accepted one gives the oracle's result on every replay (the gate is
+  cleared within each call).
+
+Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the fp32 output against oracle
+O2, as everywhere.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+from tests.fattn_cases import assert_parity, run_gpu
+
+pytestmark = pytest.mark.gpu
+SCALE = 1.0 / math.sqrt(128)
+
+
+def _case(name):
+    print(f"\n[case] {name}", flush=True)
+
+
+def _decode_check(seed):
+    # Qwen3-4B decode over 4096 cells: 32 splits per kv head on the library workspace
+    q, k, v = O.make_inputs(seed, T=1, Hq=32, Hkv=8, n_kv=4096)
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=4000)
+    assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=4000), ref, what=f"decode after masked prefill ({seed})")
+
+
+def _dst(q):
+    from arclight_amd import abi, device
+    return device.DeviceTensor.empty(q.shape, np.float32, axes=abi.DST_AXES)
+
+
+def _sampled(q, k, v, m, sel):
+    rows = (len(sel) + 63) // 64 * 64
+    ms = np.full((1, 1, rows, m.shape[3]), -np.inf, dtype=np.float16)
+    ms[:, :, :len(sel)] = m[:, :, sel]
+    return O.attention(np.ascontiguousarray(q[:, sel]), k, v, ms, scale=SCALE)
+
+
+def test_masked_single_split_prefill_then_decode(gpu):
+    from arclight_amd import fattn
+    T, pos0 = 1024, 1024
+    n_kv = pos0 + T
+    q, k, v = O.make_inputs(77, T=T, Hq=64, Hkv=8, n_kv=n_kv)
+    m = O.causal_mask(T, n_kv, pos0, kv_len=n_kv)
+    # the masked plan reserves the counter region (the gate lives there)
+    need = fattn.workspace_bytes(fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v), fattn.upload_mask(m),
+                                 None, _dst(q), scale=SCALE)
+    assert need >= 256 * 1024, need
+    rng = np.random.default_rng(5)
+    sel = np.unique(np.concatenate([[0, 63, 64, T - 1], rng.choice(T, 20, replace=False)]))
+    _case("Qwen3-32B chunk 1024, explicit causal mask (accepted, single-split fallback plan)")
+    got = run_gpu(q, k, v, m, scale=SCALE)
+    assert_parity(got[:, sel], _sampled(q, k, v, m, sel), what="32B masked chunk")
+    _case("decode after it on the library workspace")
+    _decode_check(11)
+    m2 = m.copy()
+    m2[..., 300] = -np.inf                           # a hole: the mask pass rejects it
+    _case("Qwen3-32B chunk 1024, mask with a hole (rejected)")
+    got = run_gpu(q, k, v, m2, scale=SCALE)
+    assert_parity(got[:, sel], _sampled(q, k, v, m2, sel), what="32B masked chunk with hole")
+    _case("decode after the rejected mask")
+    _decode_check(12)
+    _case("accepted mask again")
+    got = run_gpu(q, k, v, m, scale=SCALE)
+    assert_parity(got[:, sel], _sampled(q, k, v, m, sel), what="32B masked chunk again")
+
+
+def test_masked_calls_on_two_streams(gpu):
+    from arclight_amd import device, fattn
+    n_kv = 2048
+    q, k, v = O.make_inputs(4242, T=512, Hq=32, Hkv=8, n_kv=n_kv)
+    m_ok = O.causal_mask(512, n_kv, 1536, kv_len=2000)
+    m_bad = m_ok.copy()
+    m_bad[..., 100] = -np.inf
+    m_bad[..., 200:210] = np.float16(-1.5)
+    ref_ok = O.attention(q, k, v, m_ok, scale=SCALE)
+    ref_bad = O.attention(q, k, v, m_bad, scale=SCALE)
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    dm_ok, dm_bad = fattn.upload_mask(m_ok), fattn.upload_mask(m_bad)
+    sa, sb = device.Stream(), device.Stream()
+    try:
+        outs_a = [_dst(q) for _ in range(3)]
+        outs_b = [_dst(q) for _ in range(3)]
+        # one eager call per stream allocates its workspace
+        fattn.flash_attn_ext(dq, dk, dv, dm_bad, scale=SCALE, dst=outs_a[0], stream=sa)
+        fattn.flash_attn_ext(dq, dk, dv, dm_ok, scale=SCALE, dst=outs_b[0], stream=sb)
+        device.synchronize()
+        _case("two streams, rejected and accepted masks interleaved")
+        for i in range(3):
+            fattn.flash_attn_ext(dq, dk, dv, dm_bad, scale=SCALE, dst=outs_a[i], stream=sa)
+            fattn.flash_attn_ext(dq, dk, dv, dm_ok, scale=SCALE, dst=outs_b[i], stream=sb)
+        device.synchronize()
+        fattn.device_errors()
+        for i in range(3):
+            assert_parity(outs_a[i].numpy(np.float32), ref_bad, what=f"stream A (rejected mask) call {i}")
+            assert_parity(outs_b[i].numpy(np.float32), ref_ok, what=f"stream B (accepted mask) call {i}")
+    finally:
+        device.synchronize()
+        sa.destroy()
+        sb.destroy()
+
+
+def test_masked_call_replayed_with_rejected_then_accepted_mask(gpu):
+    from arclight_amd import device, fattn
+    n_kv = 1024
+    q, k, v = O.make_inputs(99, T=512, Hq=32, Hkv=8, n_kv=n_kv)
+    m_ok = O.causal_mask(512, n_kv, 512, kv_len=n_kv)
+    m_bad = m_ok.copy()
+    m_bad[..., 7] = -np.inf
+    refs = {"ok": O.attention(q, k, v, m_ok, scale=SCALE), "bad": O.attention(q, k, v, m_bad, scale=SCALE)}
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    dm = fattn.upload_mask(m_ok)
+    dst = _dst(q)
+    st = device.Stream()
+    g = None
+    try:
+        fattn.flash_attn_ext(dq, dk, dv, dm, scale=SCALE, dst=dst, stream=st)   # workspace outside the capture
+        st.synchronize()
+        g = device.Graph(st, lambda: fattn.flash_attn_ext(dq, dk, dv, dm, scale=SCALE, dst=dst, stream=st))
+        for i, which in enumerate(["bad", "ok", "ok", "bad", "ok"]):
+            _case(f"replay {i}: {which} mask")
+            dm.buf.upload(np.ascontiguousarray((m_ok if which == "ok" else m_bad).view(np.uint16)), dm.offset)
+            dst.buf.zero()
+            device.synchronize()
+            g.launch(st)
+            st.synchronize()
+            fattn.device_errors()
+            assert_parity(dst.numpy(np.float32), refs[which], what=f"replay {i} ({which} mask)")
+    finally:
+        device.synchronize()
+        if g is not None:
+            g.destroy()
+        st.destroy()
