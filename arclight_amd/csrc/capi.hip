@@ -58,13 +58,17 @@ struct DeviceState {
     int        n_cu = 0;
     int        lds_per_block = 0;
     std::map<void *, Workspace> ws;     // per stream (nullptr: the default stream)
-    int *      err = nullptr;       // kernel-recorded errors (set_rows)
+    int *      err = nullptr;       // kernel-recorded errors: this device's copy of g_err_flags
+    void *     noalloc = nullptr;   // this device's copy of `scratch` (al_fattn_f16_noalloc), once set up
 };
 
 std::mutex g_mu;
 std::vector<DeviceState> g_dev;
 
 }  // namespace
+
+// Kernel-recorded error flags (al_device_errors), one copy per GPU.
+static __device__ __align__(256) int g_err_flags[64];
 
 static int device_state(int * dev_out, DeviceState ** st_out) {
     int dev = 0;
@@ -78,10 +82,10 @@ static int device_state(int * dev_out, DeviceState ** st_out) {
         if (e != hipSuccess) return al_hip_fail(e, "hipDeviceGetAttribute");
         e = hipDeviceGetAttribute(&st.lds_per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
         if (e != hipSuccess) return al_hip_fail(e, "hipDeviceGetAttribute");
-        e = hipMalloc((void **) &st.err, 256);
-        if (e != hipSuccess) return al_hip_fail(e, "hipMalloc(error flag)");
-        e = hipMemset(st.err, 0, 256);
-        if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
+        e = hipGetSymbolAddress((void **) &st.err, HIP_SYMBOL(g_err_flags));
+        if (e != hipSuccess) return al_hip_fail(e, "hipGetSymbolAddress(error flags)");
+        e = hipMemset(st.err, 0, sizeof(g_err_flags));
+        if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flags)");
         st.init = true;
     }
     *dev_out = dev;
@@ -446,7 +450,10 @@ extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
     return pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
 }
 
-extern "C" int al_fattn_f16(const al_fattn_args * a) {
+// One call with the plan's workspace: the caller's, else the library's for
+// the stream (library_workspace), or with noalloc_ws set the no-allocation
+// entry's device array, which is never grown.
+static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_bytes) {
     int n_cu = 0, lds = 0;
     int rc = al_device_cu_count(&n_cu);
     if (rc == AL_OK) rc = al_device_lds_per_block(&lds);
@@ -457,8 +464,12 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
     const size_t need = pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
     int32_t * lims = nullptr;
     if (need) {
-        void * ws = a->workspace;
-        if (ws) {
+        void * ws = noalloc_ws ? noalloc_ws : a->workspace;
+        if (noalloc_ws) {
+            if (noalloc_bytes < need)
+                return al_fail(AL_ERR_WORKSPACE, "fattn (no allocation): the call needs %zu bytes of scratch, "
+                               "more than the %zu-byte device array", need, noalloc_bytes);
+        } else if (ws) {
             if (a->workspace_bytes < need)
                 return al_fail(AL_ERR_WORKSPACE, "fattn: workspace %llu bytes < %zu needed",
                                (unsigned long long) a->workspace_bytes, need);
@@ -499,6 +510,53 @@ extern "C" int al_fattn_f16(const al_fattn_args * a) {
     }
     if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
     return AL_OK;
+}
+
+extern "C" int al_fattn_f16(const al_fattn_args * a) { return fattn_run(a, nullptr, 0); }
+
+// ---------------------------------------------------------------------------
+// no-allocation entry point
+// ---------------------------------------------------------------------------
+
+// The scratch of al_fattn_f16_noalloc: arrival counters and gate, merge
+// records and row limits, laid out as a caller workspace. One copy per GPU,
+// held until the process ends; every call on that GPU shares it.
+static __device__ __align__(256) unsigned char scratch[AL_FATTN_NOALLOC_SCRATCH_BYTES];
+
+__global__ void zero_words_kernel(unsigned * p, int n) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+extern "C" int al_fattn_noalloc_init(void) {
+    int dev;
+    DeviceState * st;
+    int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (st->noalloc) return AL_OK;
+    void * ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return al_hip_fail(e, "hipGetSymbolAddress(scratch)");
+    // the counter region must start at zero (every call leaves it so)
+    const int words = (int) (kFattnCounterBytes / 4);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(64), dim3(256), 0, nullptr, (unsigned *) ptr, words);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) return al_hip_fail(e, "clearing the scratch counters");
+    st->noalloc = ptr;
+    return AL_OK;
+}
+
+extern "C" int al_fattn_f16_noalloc(const al_fattn_args * a) {
+    int dev;
+    DeviceState * st;
+    int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    if (!st->noalloc) {
+        rc = al_fattn_noalloc_init();
+        if (rc != AL_OK) return rc;
+    }
+    return fattn_run(a, st->noalloc, AL_FATTN_NOALLOC_SCRATCH_BYTES);
 }
 
 extern "C" const char * al_last_error(void) { return g_last_error.c_str(); }

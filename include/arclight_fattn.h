@@ -145,6 +145,27 @@ int al_fattn_f16(const al_fattn_args * args);
 /* Workspace bytes al_fattn_f16 needs for these arguments (0 if none). */
 uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
 
+/*
+ * al_fattn_f16 without any allocation. No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * validation, kernels and results as al_fattn_f16; args->workspace is
+ * ignored. The scratch (arrival counters and gate, split-KV merge records,
+ * row limits) is a file-scope device array of
+ * AL_FATTN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. A
+ * call that needs more (al_fattn_workspace_bytes) fails with
+ * AL_ERR_WORKSPACE. Every call on one GPU shares that array: calls that
+ * overlap on one GPU (two streams, or two host threads) race and may give
+ * wrong results; order them on one stream.
+ * al_fattn_noalloc_init sets up the current device (finds its copy of the
+ * array and clears the counter region, synchronizing the default stream):
+ * call it once per device before capturing a graph; otherwise the first
+ * call does it.
+ */
+#define AL_FATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+int al_fattn_noalloc_init(void);
+int al_fattn_f16_noalloc(const al_fattn_args * args);
+
 /* Message of the calling thread's most recent failure ("" if none). */
 const char * al_last_error(void);
 
