@@ -18,6 +18,7 @@ SIGNATURES = {
     # include/arclight_fattn.h
     "al_fattn_f16": (_I, [ctypes.POINTER(abi.AlFattnArgs)]),
     "al_fattn_workspace_bytes": (_U64, [ctypes.POINTER(abi.AlFattnArgs)]),
+    "al_fattn_f16_worker": (_I, [ctypes.POINTER(abi.AlFattnArgs), _I, _I]),
     "al_fattn_noalloc_init": (_I, []),
     "al_fattn_f16_noalloc": (_I, [ctypes.POINTER(abi.AlFattnArgs)]),
     "al_last_error": (ctypes.c_char_p, []),

@@ -514,6 +514,16 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
 
 extern "C" int al_fattn_f16(const al_fattn_args * a) { return fattn_run(a, nullptr, 0); }
 
+extern "C" int al_fattn_f16_worker(const al_fattn_args * a, int ith, int nth) {
+    if (nth < 1 || ith < 0 || ith >= nth) return al_fail(AL_ERR_INVALID, "fattn: worker %d of %d", ith, nth);
+    if (ith != 0) return AL_OK;                        // one launch per node
+    const int rc = fattn_run(a, nullptr, 0);
+    if (rc != AL_OK) return rc;
+    const hipError_t e = hipStreamSynchronize((hipStream_t) a->stream);
+    if (e != hipSuccess) return al_hip_fail(e, "fattn: hipStreamSynchronize");
+    return AL_OK;
+}
+
 // ---------------------------------------------------------------------------
 // no-allocation entry point
 // ---------------------------------------------------------------------------

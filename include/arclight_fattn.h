@@ -142,6 +142,20 @@ typedef struct al_fattn_args {
  */
 int al_fattn_f16(const al_fattn_args * args);
 
+/*
+ * The op as nnml's workers run it. The reference executes a graph node on
+ * every worker of the pool, each with its own (ith, nth) from its
+ * nnml_compute_state (nnml/src/scheduler.cpp:98-101 inside
+ * nnml_single_graph_compute_thread :122-146; nnml/include/thread.h:153-168),
+ * splits the rows by ith (nnml/src/ops/arm/arm.cpp:2250-2257), and puts a
+ * barrier after the node (scheduler.cpp:135-142). Here worker 0 runs
+ * al_fattn_f16 and waits for args->stream, so that barrier still means the
+ * output is complete; every other worker returns AL_OK at once without
+ * reading args or calling the HIP runtime. (ith, nth) outside
+ * 0 <= ith < nth gives AL_ERR_INVALID.
+ */
+int al_fattn_f16_worker(const al_fattn_args * args, int ith, int nth);
+
 /* Workspace bytes al_fattn_f16 needs for these arguments (0 if none). */
 uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
 
