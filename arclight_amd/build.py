@@ -27,9 +27,19 @@ CFLAGS = [
 ]
 
 
+# Per-file code generation options. The prefill kernel keeps its MFMA
+# accumulators in VGPRs, which its softmax reads directly (with AGPR
+# accumulators the compiler moves every tile's scores and output blocks
+# between the two register files).
+EXTRA_FLAGS = {
+    "fattn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src, asm_dir=None):
     obj = os.path.join(OBJDIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", src, "-o", obj]
+    extra = EXTRA_FLAGS.get(os.path.basename(src), [])
+    cmd = [HIPCC, *CFLAGS, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass does not know the device-only target feature; drop that note
     noise = "'-packed-fp32-ops' is not a recognized feature"
@@ -39,7 +49,7 @@ def _compile(src, asm_dir=None):
     if asm_dir:
         os.makedirs(asm_dir, exist_ok=True)
         out = os.path.join(asm_dir, os.path.basename(src) + ".s")
-        subprocess.run([HIPCC, *CFLAGS, "--cuda-device-only", "-S", src, "-o", out],
+        subprocess.run([HIPCC, *CFLAGS, *extra, "--cuda-device-only", "-S", src, "-o", out],
                        check=True, capture_output=True)
     return obj, err
 

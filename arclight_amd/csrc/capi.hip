@@ -173,6 +173,8 @@ struct Plan {
     // mask pass and the prefill kernel (FattnParams::row_lim)
     bool masked_prefill = false;
     int32_t prefill_tiles = 0;
+    int32_t prefill_split = 1;
+    int prefill_rows = kFattnPrefillRows;
     size_t lims_bytes = 0;
 };
 
@@ -191,6 +193,22 @@ int env_int(const char * name, int dflt) {
     const char * s = getenv(name);
     const int x = s ? atoi(s) : 0;
     return x > 0 ? x : dflt;
+}
+
+// Fewest query rows per kv head that go to the prefill kernel
+// (AL_PREFILL_MIN_ROWS); fewer take the decode or split-KV kernel.
+int prefill_min_rows() {
+    static int v = env_int("AL_PREFILL_MIN_ROWS", 256);
+    return v;
+}
+
+// Rows per prefill row tile forced by AL_PREFILL_ROWS (64 or 128); 0: by shape.
+int prefill_rows_forced() {
+    static int v = [] {
+        const int x = env_int("AL_PREFILL_ROWS", 0);
+        return x == 64 || x == 128 ? x : 0;
+    }();
+    return v;
 }
 
 int wgs_per_cu() {
@@ -318,6 +336,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     p.dst = (char *) d.data; p.dst_nb1 = d.nb[1];
     p.T = (int32_t) T; p.Hq = (int32_t) Hq; p.Hkv = (int32_t) Hkv; p.G = (int32_t) (Hq / Hkv); p.B = (int32_t) B;
     p.R = p.T * p.G;
+    p.g_magic = p.G > 1 ? (uint32_t) (((1ull << 32) + (uint64_t) p.G - 1) / (uint64_t) p.G) : 0u;
     p.rk3 = (int32_t) (B / k.ne[3]); p.rv3 = (int32_t) (B / v.ne[3]);
     p.n_kv = (int32_t) n_kv;
     p.kv_hi = (int32_t) ((a->kv_len <= 0 || a->kv_len > n_kv) ? n_kv : a->kv_len);
@@ -332,19 +351,46 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     p.m0 = powf(2.0f, -(p.max_bias) / p.n_head_log2);
     p.m1 = powf(2.0f, -(p.max_bias / 2.0f) / p.n_head_log2);
 
-    // Many query rows with implicit masking: the prefill kernel, one
-    // workgroup per 64-row tile, when that alone fills the device.
-    const int64_t prefill_tiles = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows;
-    // (it keeps the running max on scores as computed: needs scale > 0 unless softcapped)
-    const bool prefill_shape = !p.dyn && p.R > 32 && prefill_tiles * Hkv * B >= n_cu &&
+    // Many query rows: the prefill kernel, one workgroup per row tile of 128
+    // rows, or of 64 rows (two cell splits inside the workgroup) when
+    // 128-row tiles leave CUs idle; n_split workgroups per tile (each taking
+    // every n_split-th share of the 64-cell tiles of the visible range) when
+    // the row tiles alone still do not fill the device. It keeps the running
+    // max on scores as computed, so it needs scale > 0 unless softcapped.
+    const int64_t big_units = (p.R + kFattnPrefillRows - 1) / kFattnPrefillRows * Hkv * B;
+    const int prefill_rows = prefill_rows_forced() ? prefill_rows_forced()
+                             : big_units >= n_cu ? kFattnPrefillRows : kFattnPrefillRows / 2;
+    const int in_wg_split = kFattnPrefillRows / prefill_rows;
+    const int64_t prefill_tiles = (p.R + prefill_rows - 1) / prefill_rows;
+    const int64_t prefill_units = prefill_tiles * Hkv * B;
+    int64_t prefill_split = 1;
+    {
+        int64_t extent = p.kv_hi;
+        if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
+        const int64_t cell_tiles = std::max<int64_t>(1, (extent + 63) / 64);
+        while (prefill_split < kFattnPrefillMaxSplit && prefill_units * prefill_split < n_cu &&
+               cell_tiles >= 2 * in_wg_split * (prefill_split + 1))
+            ++prefill_split;
+    }
+    const bool prefill_shape = !p.dyn && p.R >= prefill_min_rows() && prefill_units <= kFattnGateWord &&
+                               (uint64_t) p.R * (uint64_t) p.G < (1ull << 32) && prefill_tiles * B <= 65535 &&
+                               (uint64_t) (n_kv + 64) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
+                               (uint64_t) (n_kv + 64) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
                                lds_per_block >= (int64_t) fattn_prefill_lds_bytes() && q_slice < INT32_MAX &&
                                (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill();
+    const size_t prefill_part = prefill_split > 1 ? (size_t) prefill_units * prefill_split * prefill_rows *
+                                                        kFattnRecordStride * sizeof(float)
+                                                  : 0;
     if (!m.data && prefill_shape) {
         pl.kernel = kPrefill;
-        pl.rows_per_tile = kFattnPrefillRows;
+        pl.rows_per_tile = prefill_rows;
         p.n_row_tiles = (int32_t) prefill_tiles;
-        p.n_split = 1;
+        p.n_split = (int32_t) prefill_split;
         p.cells_per_split = 0;
+        if (prefill_split > 1) {
+            pl.counters_bytes = kFattnCounterBytes;
+            pl.part_bytes = prefill_part;
+        }
         *out = pl;
         return AL_OK;
     }
@@ -430,10 +476,15 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     }
     if (m.data && prefill_shape) {
         // the gate lives in the counter region, which is reserved also when
-        // the split-KV plan has a single split
+        // the split-KV plan has a single split; the prefill kernel and the
+        // split-KV kernel share the counters and the records (only one of
+        // them runs past its gate)
         pl.masked_prefill = true;
         pl.prefill_tiles = (int32_t) prefill_tiles;
+        pl.prefill_split = (int32_t) prefill_split;
+        pl.prefill_rows = prefill_rows;
         pl.counters_bytes = kFattnCounterBytes;
+        pl.part_bytes = std::max(pl.part_bytes, prefill_part);
         pl.lims_bytes = ((size_t) T * p.m_ne2 * p.m_ne3 * sizeof(int32_t) + 255) / 256 * 256;
     }
     *out = pl;
@@ -492,19 +543,19 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
         hipStream_t st = (hipStream_t) a->stream;
         FattnParams pp = pl.p;
         pp.n_row_tiles = pl.prefill_tiles;
-        pp.n_split = 1;
+        pp.n_split = pl.prefill_split;
         pp.cells_per_split = 0;
         pp.row_lim = lims;
         pp.gate = gate;
         e = fattn_mask_limits_launch(pl.p, lims, gate, st);
-        if (e == hipSuccess) e = fattn_prefill_launch(pp, st);
+        if (e == hipSuccess) e = fattn_prefill_launch(pp, pl.prefill_rows, st);
         pl.p.gate = gate;
         if (e == hipSuccess) e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, st);
         if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
         return AL_OK;
     }
     switch (pl.kernel) {
-        case kPrefill: e = fattn_prefill_launch(pl.p, (hipStream_t) a->stream); break;
+        case kPrefill: e = fattn_prefill_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
         case kDecode:  e = fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream); break;
         default:       e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
     }

@@ -366,10 +366,11 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         for (int rb = 0; rb < RB; ++rb) {
             if (ws == 0 && rvalid[rb]) {
                 float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok[rb]) * p.Hq + head[rb]) * p.dst_nb1);
+                const RowScale rs = row_scale(m_run[rb], l_run[rb], p.sinks, head[rb]);
 #pragma unroll
                 for (int mb = 0; mb < 8; ++mb)
-                    *(float4 *) (out + 16 * mb + 4 * g) = finalize4(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]},
-                                                                    m_run[rb], l_run[rb], p.sinks, head[rb]);
+                    *(float4 *) (out + 16 * mb + 4 * g) =
+                        apply_scale(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]}, rs);
             }
         }
         return;

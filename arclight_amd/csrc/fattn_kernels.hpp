@@ -18,6 +18,7 @@ struct FattnParams {
     char * dst;         int64_t dst_nb1;                 // f32 rows (i3*T + i1)*Hq + i2
 
     int32_t T, Hq, Hkv, G, B, R;    // R = T*G query rows per kv head
+    uint32_t g_magic;               // ceil(2^32 / G) (0 for G = 1): r / G = umulhi(r, g_magic) for r G < 2^32
     int32_t rk3, rv3;               // q streams per k / v stream
     int32_t n_kv;                   // cells addressable in k/v
     int32_t kv_hi;                  // cells >= kv_hi are masked for all rows
@@ -52,14 +53,18 @@ int fattn_splitkv_rows_per_tile(int R);
 int fattn_splitkv_waves(int rows_per_tile);
 hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
 
-// Prefill kernel: 64-row tiles, one workgroup per (kv head, row tile,
-// stream); needs fattn_prefill_lds_bytes() of LDS. Masking is the implicit
+// Prefill kernel: row tiles of rows_per_tile = 128 or 64 query rows (64:
+// two cell splits within the workgroup), n_split workgroups per (kv head,
+// row tile, stream) (1..kFattnPrefillMaxSplit; with more than one, merge
+// records of rows_per_tile rows and arrival counters in the workspace);
+// needs fattn_prefill_lds_bytes() of LDS. Masking is the implicit
 // length / causal rule, optionally narrowed per row by the row limits that
 // the mask pass (fattn_mask_limits_launch) derives from a mask tensor.
-hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream);
+hipError_t fattn_prefill_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
 hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream);
 size_t fattn_prefill_lds_bytes();
-constexpr int kFattnPrefillRows = 64;
+constexpr int kFattnPrefillRows = 128;          // query rows per workgroup (at most)
+constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row tile
 
 // Decode kernel: up to 16 query rows per kv head, one kv head per
 // workgroup, `waves` wavefronts each streaming 16-cell stages of K/V through

@@ -1,469 +1,594 @@
 // Prefill (and long speculative-verify) attention for gfx950: many query rows
-// per kv head, causal / length masking given implicitly (kv_len,
-// causal_pos0). Semantics as nnml_compute_forward_flash_attn_ext_f16
+// per kv head, masking given by the length / causal rule (kv_len,
+// causal_pos0) and optionally narrowed per row by the mask pass's row limits.
+// Semantics as nnml_compute_forward_flash_attn_ext_f16
 // (nnml/src/ops/arm/arm.cpp:2196-2433), numerics as fattn_splitkv.hip.
 //
-// One workgroup = one row tile of 64 query rows of one kv-head group
-// (row r -> token r / G, head kvh*G + r % G) and 8 wavefronts, two per SIMD.
-// Wave w takes row half w & 1 (32 rows: 2 MFMA row blocks, so each K/V
-// operand read from LDS feeds 2 MFMAs) and cell split w >> 1 (every 4th
-// 32-cell tile of the visible range). The two waves of a split sit on
-// different SIMDs and share the split's ring of two 16 KiB LDS stages: each
-// loads half of every tile, publishes "my half landed" in an LDS flag, reads
-// the whole tile once the other's half has landed, publishes "stage read",
-// and refills its half of the stage once the other has read it too. (With
-// one wave loading whole tiles the other waited for it on every tile.)
-// No workgroup barrier runs in the loop, so the splits drift apart and the
-// two waves on each SIMD (different splits) overlap each other's matrix and
-// vector work. A 512-token chunk of Qwen3-4B gives 32 row tiles x 8 kv heads
-// = 256 workgroups, one per CU.
+// Work decomposition. One workgroup per CU: 4 computing wavefronts, one
+// per SIMD, each holding 32 query rows of one kv-head group (row r ->
+// token r / G, head kvh*G + r % G; one 32x32 MFMA block), and 4 producer
+// wavefronts (one per SIMD too) that only move K/V tiles into LDS: an
+// LDS-DMA instruction stalls the wave that issues it for tens of cycles, so
+// the computing waves issue none. RG of the computing waves (the row
+// groups) hold different rows and walk the same 64-cell tiles, sharing each
+// tile through LDS; the other 4 / RG do the same for another cell split
+// (tiles s, s + SP, ...), and the splits merge their softmax states through
+// LDS at the end. RG = 4 (128 rows, one split) halves the L2 -> LDS traffic
+// per MFMA; RG = 2 (64 rows, two splits) gives twice the workgroups for
+// calls with few rows. When even that does not fill the device, n_split
+// workgroups share a row tile and the last to arrive combines their merge
+// records (the split-KV kernel's record / counter scheme).
 //
-// K/V tiles travel HBM/L2 -> LDS by LDS-DMA buffer loads:
-//   - K as MFMA A operands: block (mb, kb) holds, at lane l's 16-byte slot,
-//     cell 16 mb + l % 16, dims 32 kb + 8 (l / 16) .. + 7, so ds_read_b128
-//     at lane*16 yields the operand;
-//   - V cell-major (256 bytes per cell) with the 16-byte granule j of cell c
-//     at slot j ^ (c & 15), read transposed by ds_read_b64_tr_b16 into V^T
-//     A operands whose k slots follow the S^T output layout (cells 4g + i
-//     and 16 + 4g + i of lane group g), so P^T is S^T in place.
-// The DMA is inline assembly the compiler does not count; each wave waits
-// for its own half (s_waitcnt vmcnt) before publishing it. The query rows
-// come the same way, once per workgroup, into a staging area that holds the
-// flags afterwards.
+// Per computing wave and tile (f16 MFMA 32x32x16, f32 accumulation):
+//   S^T[64 cells x 32 rows]  = K Q^T     16 MFMA (two 32-cell blocks, 8 k-steps)
+//   O^T[128 dims x 32 rows] += V^T P^T   16 MFMA (four 32-dim blocks, 4 k-steps)
+// The S^T accumulator layout (lane l: row l % 32, cells (v % 4) + 8 (v / 4)
+// + 4 (l / 32) of register v) is the P^T operand layout of PV when the k
+// slots of each 16-cell step are ordered accordingly, so P^T is S^T in
+// place; V^T operands follow the same order, read by ds_read_b64_tr_b16.
 //
-// Softmax per tile: the running max is kept on the raw scores (scale > 0
-// keeps their order), p = exp2(s * c - m * c) with c = scale * log2(e) is
-// one FMA and one v_exp_f32 per score, P is packed to f16 two at a time,
-// and the row sums l come from an extra MFMA against an all-ones operand
-// (f32 accumulation of the same f16 P that weights V). The reference max
-// moves lazily (only when a tile exceeds it by more than kTau in natural
-// units), so O is rarely rescaled; the rescale runs outside the fast loop so
-// the accumulators stay in place across iterations.
+// Software pipeline: iteration i runs QK^T of tile i + 1 on the matrix
+// cores while the vector ALU turns the scores of tile i into probabilities,
+// then PV of tile i; the slots of both phases are ordered explicitly (LDS
+// reads prefetched one or two slots ahead, exponentials pinned to their
+// slot), so the two units overlap within each wave. Softmax: the running
+// max is kept on raw scores (scale > 0 keeps their order), p = exp2(s c -
+// m c) with c = scale log2(e), row sums accumulate by v_dot2 of the f16 P
+// with ones, and the reference max moves lazily (only when a tile exceeds
+// it by more than kTau in natural units) on a cold path outside the fast
+// loop, so the O accumulators stay in the matrix cores' registers there.
 //
-// The 1-D grid runs kv head fastest (XCD affinity: with Hkv = 8 each head's
-// K/V stays in one XCD's L2) and, with a causal mask, row tiles longest
-// first.
+// Memory path. K and V tiles go HBM/L2 -> LDS by LDS-DMA (buffer_load ...
+// lds), each producer moving the share of its computing partner (1 / RG of
+// every tile of its split), into per-split rings of NK K buffers and NV V
+// buffers (RG = 2: 2 and 3; RG = 4: 4 and 6; 160 KiB in all). K(i + NK) is
+// issued once iteration i starts (its buffer held K(i), read in iteration
+// i - 1) and V(i + NV - 1) likewise, so every tile has one or more
+// iterations to land; one workgroup barrier per iteration publishes them.
+// Tiles are cell-major, 256 bytes per cell, with 16-byte granules permuted
+// within a cell so that the operand reads are free of bank conflicts: K
+// granule j of cell c at slot j ^ (c & 15) (a K operand read covers 32
+// cells x 16 bytes), V granule j at slot j ^ 4 (c & 3) (a transposing V
+// read covers 4 cells x 64 bytes). The K/V views end at the workgroup's
+// last visible cell, so cells that no row sees read as zeros (unwritten
+// cache cells may hold non-finite values). The query rows go straight
+// into the computing waves' registers; the output rows leave through LDS,
+// 16 bytes per lane over whole rows.
 
-#include "fattn_tile.hpp"
+#include <type_traits>
+
+#include "fattn_prefill_common.hpp"
 
 namespace {
 
-using namespace fattn;
+using namespace fattn_prefill;
 
-constexpr int kCS = 4;                       // cell splits: tiles cs, cs + 4, ...
-constexpr int kRH = 2;                       // row halves
-constexpr int kPW = kCS * kRH;               // waves per workgroup
-constexpr int kPRB = 2;                      // MFMA row blocks per wave
-constexpr int kPRows = 16 * kPRB * kRH;      // query rows per workgroup
-constexpr int kKBytes = 8 * 1024;            // K of a 32-cell tile: 8 MFMA-ordered 1 KiB blocks
-constexpr int kStage = 2 * kKBytes;          // K then V (32 cells x 256 bytes)
-constexpr int kNB = 2;                       // stages per split
-constexpr int kStride = kCS * 32;            // cells between a split's tiles
-constexpr int kRing = kCS * kNB * kStage;    // 128 KiB
-constexpr int kQBytes = kPRows * 512;        // the tile's query rows, f32 (32 KiB)
-constexpr int kRec = kPRows * kRowStride * 4;        // one split's merge record (64 rows)
-constexpr int kLds = kCS * kRec > kRing + kQBytes ? kCS * kRec : kRing + kQBytes;   // 160 KiB
-constexpr float kLog2e = 1.44269504088896341f;
-constexpr int kSpinLimit = 1 << 22;          // flag polls before a wave gives up (never in a correct run)
+constexpr int kTC = 64;                          // cells per tile
+constexpr int kTileBytes = kTC * 256;            // one tile of K or of V (16 KiB)
+static_assert(kLds == 10 * kTileBytes, "10 tiles fill the LDS");
+static_assert(80 * 1024 + 128 * 512 <= kLds && 64 * kFattnRecordStride * 4 <= 80 * 1024, "output staging fits past the merge records");
 
-// The operands of one tile in registers.
-struct TileOps {
-    u32x4 k[2][4];                           // K A operands [mb][kb]
-    half8 vt[8];                             // V^T A operands, dim block d
+// Shape of a workgroup with RG row groups: SP cell splits; per split a ring
+// of NK K buffers and NV V buffers; PER LDS-DMA instructions per wave and
+// tile (each wave of a split moves 1 / RG of every tile).
+template <int RG>
+struct Shape {
+    static constexpr int SP = kWaves / RG;
+    static constexpr int ROWS = 32 * RG;
+    static constexpr int NK = RG == 4 ? 4 : 2;
+    static constexpr int NV = RG == 4 ? 6 : 3;
+    static constexpr int RING = (NK + NV) * kTileBytes;
+    static constexpr int PER = kTileBytes / 1024 / RG;
+    static_assert(SP * RING == kLds, "the rings fill the LDS");
+    static_assert(NV > NK && PER % 4 == 0, "V runs further ahead than K; whole DMA instructions per slot");
 };
 
-// LDS-DMA of half h of tile (cells cb ..) into a stage: the 4 K blocks of
-// cell block mb = h, then V blocks 4h .. 4h + 3 (cells 16h .. 16h + 15).
-__device__ __forceinline__ void issue_half(const int4v kd, const int4v vd, const uint32_t base, const uint32_t cb,
-                                           const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n,
-                                           const int h) {
-    const uint32_t kofs = (cb + (uint32_t) n) * k_nb1 + (uint32_t) (g * 16) + (uint32_t) (16 * h) * k_nb1;
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-        dma16(kd, kofs + (uint32_t) (64 * kb), base + (uint32_t) ((h * 4 + kb) * 1024));
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-        const int i = 4 * h + ii;
-        const int c = 4 * i + g;
-        dma16(vd, (cb + (uint32_t) c) * v_nb1 + (uint32_t) (((n ^ c) & 15) * 16), base + (uint32_t) (kKBytes + i * 1024));
-    }
+// A pointer the wave holds alike in every lane, kept in SGPRs.
+__device__ __forceinline__ const char * uniform_ptr(const char * q) {
+    const uint64_t a = (uint64_t) q;
+    const uint64_t lo = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) a);
+    const uint64_t hi = (uint32_t) __builtin_amdgcn_readfirstlane((int) (uint32_t) (a >> 32));
+    return (const char *) (lo | (hi << 32));
 }
 
-// Both operands of a stage: K at lane*16 of each block; V^T from source
-// cells 4g + (n >> 2) (k slots 0..3) and 16 + 4g + (n >> 2) (4..7), dims
-// 16d + 4(n & 3) .. + 3 (granule 2d + ((n & 3) >> 1), half n & 1).
-__device__ __forceinline__ void read_tile(TileOps & t, const char * st, const int lane, const int g, const int n) {
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) t.k[mb][kb] = *(const u32x4 *) (st + (mb * 4 + kb) * 1024 + lane * 16);
-    const int vc0 = 4 * g + (n >> 2);
-    const int vc1 = 16 + vc0;
-    const int vq = (n & 3) >> 1;
-    const char * r0 = st + kKBytes + vc0 * 256 + (n & 1) * 8;
-    const char * r1 = st + kKBytes + vc1 * 256 + (n & 1) * 8;
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-        const half4 a = lds_read_tr16(r0 + (((2 * d + vq) ^ (vc0 & 15)) << 4));
-        const half4 c = lds_read_tr16(r1 + (((2 * d + vq) ^ (vc1 & 15)) << 4));
-        t.vt[d] = half8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
-    }
+// raw_desc of values the wave holds alike in every lane, kept in SGPRs
+__device__ __forceinline__ int4v uniform_desc(const char * base, const uint32_t bytes) {
+    const uint64_t a = (uint64_t) base;
+    return int4v{__builtin_amdgcn_readfirstlane((int) (uint32_t) a), __builtin_amdgcn_readfirstlane((int) (uint32_t) (a >> 32)),
+                 __builtin_amdgcn_readfirstlane((int) bytes), 0x00020000};
 }
 
-// LDS flag hand-off between the two waves of a split.
-__device__ __forceinline__ void flag_set(int * f, int v) {
-    __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-// Waits until *f >= v; false if it never got there (a broken hand-off),
-// so the wave ends instead of hanging.
-__device__ __forceinline__ bool flag_wait(const int * f, int v) {
-    for (int i = 0; i < kSpinLimit; ++i) {
-        if (__hip_atomic_load(const_cast<int *>(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= v) return true;
-        __builtin_amdgcn_s_sleep(1);
-    }
-    return false;
-}
-
-// First cell of a split's it-th tile: the split walks its tiles starting at
-// tile rot (0 <= rot < nt) and wrapping around, so the workgroups of one kv
-// head (which share its K/V through one XCD's L2) are spread over the cell
-// range instead of all missing the same lines at the same time.
-__device__ __forceinline__ int tile_cell(const int cb0, const int it, const int rot, const int nt) {
-    const int j = it + rot;
-    return cb0 + (j < nt ? j : j - nt) * kStride;
-}
-
-// After the softmax of tile it, a wave refills its half of the tile's stage
-// with tile it + 2 once the other wave has read the stage (its own reads are
-// complete: the wave waited for them before publishing its own "read").
-__device__ __forceinline__ bool refill(const int h, const int it, const int nt, const int rot, const int * done,
-                                       const int4v kd, const int4v vd, const uint32_t ring_addr, const int cb0,
-                                       const uint32_t k_nb1, const uint32_t v_nb1, const int g, const int n) {
-    if (it + 2 >= nt) return true;
-    const bool ok = flag_wait(done, it);
-    if (ok) issue_half(kd, vd, ring_addr + (uint32_t) ((it & 1) * kStage), (uint32_t) tile_cell(cb0, it + 2, rot, nt),
-                       k_nb1, v_nb1, g, n, h);
-    return ok;
-}
-
-// P = exp2(s c - m c) in f16, then O^T += V^T P^T and l += 1 P^T.
-__device__ __forceinline__ void accumulate_tile(TileOps & t, const floatx4 (&s)[kPRB][2], const bool full,
-                                                const bool (&vis_any)[8], const float (&m_run)[kPRB], const float cexp,
-                                                const half8 ones, const int g, floatx4 (&o)[kPRB][8],
-                                                floatx4 (&lacc)[kPRB]) {
-    half8 pf[kPRB];
-#pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-        const float mc = (m_run[rb] == -AL_INF) ? 0.0f : m_run[rb] * cexp;
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            pf[rb][j] = (_Float16) __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][j >> 2][j & 3], cexp, -mc));
-    }
-    if (!full) {
-        // cells masked for every row contribute exact zeros, whatever their V holds
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint64_t bal = __ballot(vis_any[j]);
-            if (((bal >> (16 * g)) & 0xffffull) == 0) {
-#pragma unroll
-                for (int d = 0; d < 8; ++d) t.vt[d][j] = (_Float16) 0.0f;
-            }
-        }
-    }
-#pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[rb][d] = mfma_16x16x32(t.vt[d], pf[rb], o[rb][d]);
-        lacc[rb] = mfma_16x16x32(ones, pf[rb], lacc[rb]);
-    }
-}
-
-template <bool SOFTCAP>
-__global__ __launch_bounds__(kPW * 64) void fattn_prefill_kernel(const FattnParams p) {
+template <int RG, bool SOFTCAP>
+__global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const FattnParams p) {
+    using S = Shape<RG>;
+    constexpr int ROWS = S::ROWS, NK = S::NK, NV = S::NV, PER = S::PER;
     __shared__ __attribute__((aligned(1024))) char lds[kLds];
 
+    // Waves 0..3 compute (one per SIMD); waves 4..7 (one per SIMD too) only
+    // move K/V tiles and query rows into LDS: an LDS-DMA instruction stalls
+    // the wave that issues it, so the computing waves issue none. Wave w and
+    // its producer w + 4 share the role w & 3: row group role % RG of cell
+    // split role / RG. Every barrier below is reached by all eight waves.
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rh = wave & 1;                     // row half: rows 32 rh .. 32 rh + 31 of the tile
-    const int cs = wave >> 1;                    // cell split: tiles cs, cs + kCS, ...
-    const int g = lane >> 4;
-    const int n = lane & 15;
+    const bool producer = wave >= kWaves;
+    const int role = wave & (kWaves - 1);
+    const int rg = role % RG;                    // row group: rows 32 rg .. 32 rg + 31 of the tile
+    const int si = role / RG;                    // cell split within the workgroup
+    const int h = lane >> 5;                     // half of the wave (k slots 8h .. 8h + 7)
+    const int lr = lane & 31;                    // this lane's row within the wave's 32
 
-    int id = blockIdx.x;
-    const int kvh = id % p.Hkv;
-    id /= p.Hkv;
-    const int rt = p.causal_pos0 >= 0 ? p.n_row_tiles - 1 - id % p.n_row_tiles : id % p.n_row_tiles;
-    const int b = id / p.n_row_tiles;
-    const int row0 = rt * kPRows;
-    const int rows_here = min(kPRows, p.R - row0);
-    const int t_last = (row0 + rows_here - 1) / p.G;
+    // Grid (kv head, workgroup split, row tile + stream): kv head fastest
+    // (XCD affinity: with Hkv = 8 each head's K/V stays in one XCD's L2),
+    // row tiles longest first with a causal mask. No integer division on
+    // the way to the first loads except for several streams.
+    const int kvh = blockIdx.x;
+    const int sx = blockIdx.y;                   // workgroup split of the row tile
+    const int z = blockIdx.z;
+    const int zt = p.B == 1 ? z : __builtin_amdgcn_readfirstlane(z % p.n_row_tiles);
+    const int b = p.B == 1 ? 0 : __builtin_amdgcn_readfirstlane(z / p.n_row_tiles);
+    const int rt = p.causal_pos0 >= 0 ? p.n_row_tiles - 1 - zt : zt;
+    const int row0 = rt * ROWS;
+    const int rows_here = min(ROWS, p.R - row0);
+    // row r of the kv head: token r / G, head kvh G + r % G
+    auto tok_of = [&](const int r) { return p.G == 1 ? r : (int) __umulhi((uint32_t) r, p.g_magic); };
+
+    // Last visible cell of a row: the length / causal rule, narrowed by the
+    // mask pass's row limits when a mask tensor came with the call.
+    auto row_lim = [&](const int rr) {                    // rr: row within the tile, < rows_here
+        const int r = row0 + rr;
+        const int tok = tok_of(r);
+        int lim = p.kv_hi - 1;
+        if (p.causal_pos0 >= 0) lim = (int) min((int64_t) lim, p.causal_pos0 + tok);
+        if (p.row_lim) {
+            const int hq = kvh * p.G + (r - tok * p.G);
+            lim = min(lim, p.row_lim[((int64_t) (b % p.m_ne3) * p.m_ne2 + hq % p.m_ne2) * p.T + tok]);
+        }
+        return lim;
+    };
+    // this lane's row and limit; the wave's smallest limit over its valid
+    // rows (a tile within it is visible to every row of the wave); hi_wg,
+    // one past the last cell any row of the workgroup sees (every wave
+    // evaluates all rows: no LDS before the rings fill)
+    const int rr = 32 * rg + lr;
+    const bool rvalid = rr < rows_here;
+    const int lim = rvalid ? row_lim(rr) : INT32_MAX;
+    int lim_min = lim, lim_max = -1;
+#pragma unroll
+    for (int q = 0; q < RG; ++q)
+        if (32 * q + lr < rows_here) lim_max = max(lim_max, q == rg ? lim : row_lim(32 * q + lr));
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        lim_min = min(lim_min, __shfl_xor(lim_min, off));
+        lim_max = max(lim_max, __shfl_xor(lim_max, off));
+    }
+    lim_min = __builtin_amdgcn_readfirstlane(lim_min);
+    const int hi_wg = __builtin_amdgcn_readfirstlane(lim_max) + 1;
+
+    // Tiles of the whole row tile: NT of 64 cells; split s_all of n_all
+    // takes tiles j n_all + s_all, visited from j = rot on. All splits run
+    // NI iterations (a split with one tile fewer runs its last iteration on
+    // a tile past hi_wg, which every row masks). Tiles from NI on point past
+    // the end of the K/V views: they read zeros without memory traffic.
+    const int n_all = p.n_split * S::SP;
+    const int s_all = sx * S::SP + si;
+    const int NT = (max(hi_wg, 0) + kTC - 1) / kTC;
+    const int NI = __builtin_amdgcn_readfirstlane((NT + n_all - 1) / n_all);
+    const int rot = __builtin_amdgcn_readfirstlane(NI > 0 ? (rt * NI) / p.n_row_tiles : 0);
+    const int n_vis = max(min(hi_wg, p.n_kv), 1);
+    auto tile_c0 = [&](const int i) {                     // branch-free: selects only
+        int j = i + rot;
+        j = j < NI ? j : j - NI;
+        const int c0 = (j * n_all + s_all) * kTC;
+        return i < NI ? c0 : n_vis;
+    };
+
+    // this split's ring: K(t) in K buffer t % NK, V(t) in V buffer t % NV
+    const int kring = si * S::RING, vring = kring + NK * kTileBytes;
+    auto kbuf = [&](const int t) { return kring + (t % NK) * kTileBytes; };
+    auto vbuf = [&](const int t) { return vring + (t % NV) * kTileBytes; };
+    const uint32_t lds0 = lds_addr(lds);
+
     // gated behind the mask pass: the split-KV kernel takes a rejected mask
     if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
-    int hi = p.kv_hi;
-    if (p.causal_pos0 >= 0) hi = (int) min((int64_t) hi, p.causal_pos0 + t_last + 1);
-    // with a mask tensor, each row's last visible cell from the mask pass;
-    // lane l takes row l of the tile, the workgroup's cells end after the
-    // largest of them
-    auto mask_lim = [&](const int rr) {
-        const int r = row0 + rr;
-        const int hq = kvh * p.G + r % p.G;
-        return p.row_lim[((int64_t) (b % p.m_ne3) * p.m_ne2 + hq % p.m_ne2) * p.T + r / p.G];
-    };
-    if (p.row_lim) {
-        int mx = mask_lim(min(lane, rows_here - 1));
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mx = max(mx, __shfl_xor(mx, off));
-        hi = __builtin_amdgcn_readfirstlane(min(hi, mx + 1));          // the same in every lane
-    }
 
-    const char * kbase = p.k + (int64_t) (b / p.rk3) * p.k_nb3 + (int64_t) kvh * p.k_nb2;
-    const char * vbase = p.v + (int64_t) (b / p.rv3) * p.v_nb3 + (int64_t) kvh * p.v_nb2;
-    const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
-    const int4v kd = raw_desc(kbase, (uint32_t) (p.n_kv - 1) * k_nb1 + 256);
-    const int4v vd = raw_desc(vbase, (uint32_t) (p.n_kv - 1) * v_nb1 + 256);
-
-    // this split's tiles: cells cb0 + i * kStride, i < nt, in the order of tile_cell
-    const int cb0 = cs * 32;
-    const int nt = cb0 < hi ? (hi - cb0 + kStride - 1) / kStride : 0;
-    const int rot = nt > 0 ? (int) (((int64_t) rt * nt) / p.n_row_tiles) : 0;
-    const char * ring = &lds[cs * kNB * kStage];
-    const uint32_t ring_addr = lds_addr(ring);
-
-    // The tile's query rows travel once, by LDS-DMA into the staging area
-    // behind the rings, ahead of the first K/V tiles: wave w loads rows
-    // 8w .. 8w + 7 (block i = rows 2i, 2i + 1 of 512 bytes each). Granule j
-    // of row r sits at slot j ^ 2(r & 15), which spreads the reads below over
-    // the LDS banks.
-    char * qst = &lds[kRing];
-    {
-        const int4v qd = raw_desc(p.q + (int64_t) b * p.q_nb3, p.q_bytes);
-        const uint32_t qslot = (uint32_t) (lane & 31);
+    // ---- producer waves ----
+    if (producer) {
+        // K/V views end at the workgroup's last visible cell: loads past it read zeros
+        const int bk = p.rk3 == 1 ? b : __builtin_amdgcn_readfirstlane(b / p.rk3);
+        const int bv = p.rv3 == 1 ? b : __builtin_amdgcn_readfirstlane(b / p.rv3);
+        const char * kbase = uniform_ptr(p.k + (int64_t) bk * p.k_nb3 + (int64_t) kvh * p.k_nb2);
+        const char * vbase = uniform_ptr(p.v + (int64_t) bv * p.v_nb3 + (int64_t) kvh * p.v_nb2);
+        const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
+        const uint32_t k_lim = __builtin_amdgcn_readfirstlane((uint32_t) (n_vis - 1) * k_nb1 + 256);
+        const uint32_t v_lim = __builtin_amdgcn_readfirstlane((uint32_t) (n_vis - 1) * v_nb1 + 256);
+        // LDS-DMA instruction j of this role's 1 / RG of tile t: cells
+        // cw + 4 j + (0..3) of the tile, cw = (64 / RG) rg; lane l fetches
+        // granule (l & 15) ^ perm of cell 4 j + l / 16 of them (K: perm =
+        // cell & 15, V: perm = 4 (cell & 3)), which lands at slot l & 15. The
+        // lane offsets repeat every four instructions (K) or are all alike
+        // (V); the cell offset goes into the descriptor, whose view ends at
+        // the last visible cell (zero-length past it). The offsets stay below
+        // 2^32 (the plan checks the K/V views).
+        const int cw = (kTC / RG) * rg;
+        uint32_t k_lane[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 8 * wave + 2 * i + (lane >> 5);
-            const int rq = r < rows_here ? r : 0;
-            const uint32_t qofs = (uint32_t) (((row0 + rq) / p.G) * p.q_nb1 + (kvh * p.G + (row0 + rq) % p.G) * p.q_nb2);
-            dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r & 15))) & 31) * 16,
-                  lds_addr(qst) + (uint32_t) ((8 * wave + 2 * i) * 512));
-        }
-    }
-    if (nt > 0) issue_half(kd, vd, ring_addr, (uint32_t) tile_cell(cb0, 0, rot, nt), k_nb1, v_nb1, g, n, rh);
-    if (nt > 1) issue_half(kd, vd, ring_addr + kStage, (uint32_t) tile_cell(cb0, 1, rot, nt), k_nb1, v_nb1, g, n, rh);
-    wait_later<2, 8>(min(nt, 2));                                     // own query rows landed
-    __syncthreads();                                                   // everyone's
-
-    // query rows held by this lane (column n of its two row blocks) and their
-    // Q^T B-operand fragments (k slots of block kb, group g = dims 32kb + 8g..+8)
-    int tok[kPRB];
-    bool rvalid[kPRB];
-    half8 qf[kPRB][4];
+        for (int q = 0; q < 4; ++q)
+            k_lane[q] = (uint32_t) (lane >> 4) * k_nb1 + (uint32_t) (((lane & 15) ^ ((4 * q + (lane >> 4)) & 15)) * 16);
+        const uint32_t v_lane = (uint32_t) (lane >> 4) * v_nb1 + (uint32_t) (((lane & 15) ^ (4 * ((lane >> 4) & 3))) * 16);
+        auto dma_k = [&](const int t) {
+            const uint32_t off_t = (uint32_t) (tile_c0(t) + cw) * k_nb1;
 #pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-        const int rr = 32 * rh + 16 * rb + n;
-        rvalid[rb] = rr < rows_here;
-        tok[rb] = rvalid[rb] ? (row0 + rr) / p.G : 0;
-        const char * qrow = qst + rr * 512;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const int j = 2 * (4 * kb + g);                               // granules j, j + 1 of row rr
-            const float4 qa = *(const float4 *) (qrow + ((j ^ (2 * n)) & 31) * 16);
-            const float4 qb = *(const float4 *) (qrow + (((j + 1) ^ (2 * n)) & 31) * 16);
-            qf[rb][kb] = rvalid[rb] ? to_half8(qa, qb) : half8{0, 0, 0, 0, 0, 0, 0, 0};
-        }
-    }
-    // the staging area becomes the flags: landed[cs][rh], then done[cs][rh]
-    int * flags = (int *) qst;
-    __syncthreads();
-    if (threadIdx.x < 4 * kCS) flags[threadIdx.x] = -1;
-    __syncthreads();
-    int * landed = flags + 2 * cs + rh;                               // own half landed
-    const int * landed_o = flags + 2 * cs + (rh ^ 1);                 // the other wave's half
-    int * done_m = flags + 2 * kCS + 2 * cs + rh;                     // own reads of the stage done
-    const int * done = flags + 2 * kCS + 2 * cs + (rh ^ 1);
-
-    int lim[kPRB];
-#pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) lim[rb] = row_limit(p, hi, rvalid[rb], tok[rb]);
-    int lim_min = row_limit(p, hi, true, (row0 + min(32 * rh, rows_here - 1)) / p.G);   // this wave's first token
-    if (p.row_lim) {
-        // the mask's limits, within the length / causal ones; lim_min: the
-        // smallest over the wave's valid rows
-        int mn = INT32_MAX;
-#pragma unroll
-        for (int rb = 0; rb < kPRB; ++rb) {
-            if (rvalid[rb]) lim[rb] = min(lim[rb], mask_lim(32 * rh + 16 * rb + n));
-            mn = min(mn, rvalid[rb] ? lim[rb] : INT32_MAX);
-        }
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) mn = min(mn, __shfl_xor(mn, off));
-        lim_min = __builtin_amdgcn_readfirstlane(mn);
-    }
-
-    // p = exp2(s * cexp - m * cexp); the max is tracked on s as computed
-    // (raw dot products, or softcapped scores in natural units)
-    const float cexp = SOFTCAP ? kLog2e : p.scale * kLog2e;
-    const float tau = kTau * kLog2e / cexp;                           // kTau in units of s
-    half8 ones;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ones[j] = (_Float16) 1.0f;
-
-    floatx4 o[kPRB][8];
-    floatx4 lacc[kPRB];
-    float m_run[kPRB];
-#pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-        m_run[rb] = -AL_INF;
-        lacc[rb] = floatx4{0, 0, 0, 0};
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[rb][d] = floatx4{0, 0, 0, 0};
-    }
-
-    // Tile state shared by the fast loop and the rescale path below.
-    TileOps t;
-    floatx4 s[kPRB][2];
-    float mt[kPRB];
-    bool full = true;
-    bool vis_any[8];
-    bool ok = true;
-
-    // The fast loop never scales O: a tile whose max would move the
-    // reference (the first tile always does) leaves it, and the scaling
-    // happens outside, so the accumulators stay in MFMA registers across
-    // iterations instead of being copied for a rarely taken branch.
-    int it = 0;
-    while (it < nt && ok) {
-        for (; it < nt; ++it) {
-            // tile it in its stage: own half landed (vmcnt), the other's by its flag
-            wait_later<1, 8>(it + 1 < nt ? 1 : 0);
-            flag_set(landed, it);
-            if (!flag_wait(landed_o, it)) {
-                ok = false;
-                break;
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t off = off_t + (uint32_t) (4 * j) * k_nb1;
+                dma16(uniform_desc(kbase + off, off < k_lim ? k_lim - off : 0u), k_lane[j & 3],
+                      lds0 + (uint32_t) (kbuf(t) + (cw + 4 * j) * 256));
             }
-            read_tile(t, ring + (it & 1) * kStage, lane, g, n);
-            mem_barrier();
-            __builtin_amdgcn_s_waitcnt(0xC00F | (7 << 4));                 // lgkmcnt(0): the stage is read
-            mem_barrier();
-            flag_set(done_m, it);
-            const int cb = tile_cell(cb0, it, rot, nt);
+        };
+        auto dma_v = [&](const int t) {
+            const uint32_t off_t = (uint32_t) (tile_c0(t) + cw) * v_nb1;
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t off = off_t + (uint32_t) (4 * j) * v_nb1;
+                dma16(uniform_desc(vbase + off, off < v_lim ? v_lim - off : 0u), v_lane,
+                      lds0 + (uint32_t) (vbuf(t) + (cw + 4 * j) * 256));
+            }
+        };
+        // DMA order (the waits count on it): after barrier B_i (iteration
+        // i), K(i + NK) and V(i + NV - 1); before the loop what those would
+        // have been for i = 1 - NK .. -1, interleaved the same way: RG = 2:
+        // K0 V0 K1 V1; RG = 4: V0 K0 V1 K1 V2 K2 V3 K3 V4. Before B_i: K(i + 1)
+        // and V(i) landed (2 NK - 3 tiles issued after K(i + 1) may still fly).
+        if (NI > 0) {
+            if constexpr (RG == 4) {
+                dma_v(0); dma_k(0); dma_v(1); dma_k(1); dma_v(2); dma_k(2); dma_v(3); dma_k(3); dma_v(4);
+                wait_vm<7 * PER>();               // V0, K0 landed
+            } else {
+                dma_k(0); dma_v(0); dma_k(1); dma_v(1);
+                wait_vm<3 * PER>();               // K0 landed
+            }
+        }
+        __syncthreads();                          // (1) K0 visible
+        for (int i = 0; i < NI; ++i) {
+            wait_vm<(2 * NK - 3) * PER>();
+            __syncthreads();                      // (B_i)
+            if (i + 1 < NI) {
+                dma_k(i + NK);
+                dma_v(i + NV - 1);
+            }
+        }
+        wait_vm<0>();
+        __syncthreads();                          // (3) rings free
+    }
 
-            // S^T = K Q^T: cells 4g+i (mb 0) and 16+4g+i (mb 1) of row n
+    // ---- computing waves ----
+    const float cexp = SOFTCAP ? kLog2e : p.scale * kLog2e;
+    const float tau = kTau * kLog2e / cexp;               // kTau in units of s
+    floatx16 o[4];
+    float m_run = -AL_INF, l_run = 0.0f;
+    if (!producer) {
+        // Q^T B operands: row rr (token r / G, head kvh G + r % G), dims
+        // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers
+        half8 qf[8];
+        {
+            const int r = row0 + (rvalid ? rr : 0);
+            const int tk = tok_of(r);
+            const float * qrow = (const float *) (p.q + (int64_t) b * p.q_nb3 + (int64_t) tk * p.q_nb1 +
+                                                  (int64_t) (kvh * p.G + r - tk * p.G) * p.q_nb2);
+            float4 qv[16];
 #pragma unroll
-            for (int rb = 0; rb < kPRB; ++rb)
+            for (int ks = 0; ks < 8; ++ks) {
+                qv[2 * ks] = *(const float4 *) (qrow + 16 * ks + 8 * h);
+                qv[2 * ks + 1] = *(const float4 *) (qrow + 16 * ks + 8 * h + 4);
+            }
 #pragma unroll
-                for (int mb = 0; mb < 2; ++mb) {
-                    floatx4 acc = {0, 0, 0, 0};
+            for (int ks = 0; ks < 8; ++ks)
+                qf[ks] = rvalid ? to_half8(qv[2 * ks], qv[2 * ks + 1]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+        __syncthreads();                          // (1)
+
+        // LDS read offsets of this lane: K operand (cell 32 cb + lr, granule
+        // 2 ks + h) and V^T operand (cell 16 kk + 4 h + (s16 >> 2) [+ 8],
+        // granule 4 db + 2 (q16 & 1) + ((s16 & 3) >> 1), half s16 & 1, for
+        // 16-lane group q16)
+        const int q16 = (lane >> 4) & 3, s16 = lane & 15;
+        const int vcell = 4 * h + (s16 >> 2);
+        const int vgran = 2 * (q16 & 1) + ((s16 & 3) >> 1);
+        const int vhalf = (s16 & 1) * 8;
+        const int vsw = 4 * (s16 >> 2);                   // 4 (cell & 3)
+
 #pragma unroll
-                    for (int kb = 0; kb < 4; ++kb) acc = mfma_16x16x32(as_half8(t.k[mb][kb]), qf[rb][kb], acc);
-                    s[rb][mb] = acc;
-                }
+        for (int db = 0; db < 4; ++db) o[db] = floatx16{};
+
+        auto lane_max = [&](const floatx16 (&sc)[2]) {
+            float m0 = fmaxf(fmaxf(sc[0][0], sc[0][1]), sc[0][2]);
+            float m1 = fmaxf(fmaxf(sc[1][0], sc[1][1]), sc[1][2]);
+#pragma unroll
+            for (int v = 3; v < 15; v += 2) {
+                m0 = fmaxf(fmaxf(m0, sc[0][v]), sc[0][v + 1]);
+                m1 = fmaxf(fmaxf(m1, sc[1][v]), sc[1][v + 1]);
+            }
+            return fmaxf(fmaxf(m0, sc[0][15]), fmaxf(m1, sc[1][15]));
+        };
+        auto rescale = [&](const floatx16 (&sc)[2]) {   // move the reference max of outgrown rows
+            const float mt = pair_max(lane_max(sc));
+            const bool g = mt > m_run + tau;
+            const float mn = g ? mt : m_run;
+            const float alpha = g ? __builtin_amdgcn_exp2f((m_run - mn) * cexp) : 1.0f;   // 0 from -inf
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] *= alpha;
+            l_run *= alpha;
+            m_run = mn;
+        };
+        // fresh scores: softcap, -inf for cells of a tile that some row of
+        // the wave does not wholly see, and the reference max moved when the
+        // tile outgrows it (a rare, uniform branch; the first visible tile
+        // always does)
+        auto finish_scores = [&](floatx16 (&sc)[2], const int c0) {
             if constexpr (SOFTCAP) {
 #pragma unroll
-                for (int rb = 0; rb < kPRB; ++rb)
+                for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) s[rb][j >> 2][j & 3] = p.softcap * tanhf(s[rb][j >> 2][j & 3] * p.scale);
+                    for (int v = 0; v < 16; ++v) sc[cb][v] = p.softcap * tanhf(sc[cb][v] * p.scale);
             }
-            full = cb + 31 <= lim_min;
+            if (c0 + kTC - 1 > lim_min) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vis_any[j] = true;
-            if (!full) {
+                for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) vis_any[j] = false;
-#pragma unroll
-                for (int rb = 0; rb < kPRB; ++rb)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const bool vis = cb + cell_of_slot(g, j) <= lim[rb];
-                        s[rb][j >> 2][j & 3] = vis ? s[rb][j >> 2][j & 3] : -AL_INF;
-                        vis_any[j] = vis_any[j] || vis;
+                    for (int v = 0; v < 16; ++v) {
+                        const int c = c0 + 32 * cb + (v & 3) + 8 * (v >> 2) + 4 * h;
+                        sc[cb][v] = c <= lim ? sc[cb][v] : -AL_INF;
                     }
             }
-            // lane-local maxima suffice to see that no score passes its row's
-            // reference by more than tau; the row maxima (a cross-lane
-            // reduction) are formed only on the rare path that moves it
-            bool grow_any = false;
-#pragma unroll
-            for (int rb = 0; rb < kPRB; ++rb) {
-                const float a = fmaxf(fmaxf(s[rb][0][0], s[rb][0][1]), s[rb][0][2]);
-                const float c = fmaxf(fmaxf(s[rb][0][3], s[rb][1][0]), s[rb][1][1]);
-                mt[rb] = fmaxf(fmaxf(s[rb][1][2], s[rb][1][3]), fmaxf(a, c));
-                grow_any = grow_any || (mt[rb] > m_run[rb] + tau);
-            }
-            if (__any(grow_any)) break;
-            accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-            if (!refill(rh, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n)) {
-                ok = false;
-                break;
-            }
-        }
-        if (it >= nt || !ok) break;
-        // tile `it` moves the reference max of some rows: scale, then finish it
-#pragma unroll
-        for (int rb = 0; rb < kPRB; ++rb) {
-            mt[rb] = colmax4(mt[rb]);                                     // the row's max, same in its 4 lanes
-            const bool grow = mt[rb] > m_run[rb] + tau;
-            const float mn = grow ? mt[rb] : m_run[rb];
-            const float alpha = grow ? __builtin_amdgcn_exp2f((m_run[rb] - mn) * cexp) : 1.0f;   // 0 from -inf
-            lacc[rb] *= alpha;
-#pragma unroll
-            for (int d = 0; d < 8; ++d) o[rb][d] *= alpha;
-            m_run[rb] = mn;
-        }
-        accumulate_tile(t, s, full, vis_any, m_run, cexp, ones, g, o, lacc);
-        ok = refill(rh, it, nt, rot, done, kd, vd, ring_addr, cb0, k_nb1, v_nb1, g, n);
-        ++it;
-    }
-    if (!ok && lane == 0) atomicOr(p.err + 2, 1);                      // reported by al_device_errors
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                          // no DMA may still target LDS
+            if (__any(lane_max(sc) > m_run + tau)) rescale(sc);
+        };
+        auto k_read = [&](const int kbo, const int cb, const int ks) {
+            const int c = 32 * cb + lr;
+            return as_half8(*(const u32x4 *) (lds + kbo + c * 256 + (((2 * ks + h) ^ (c & 15)) << 4)));
+        };
+        auto v_read = [&](const int vbo, const int kk, const int db) {
+            const char * vt = lds + vbo;
+            const int cbase = 16 * kk + vcell;
+            const int g = 4 * db + vgran;
+            const half4 a = lds_read_tr16(vt + cbase * 256 + ((g ^ vsw) << 4) + vhalf);
+            const half4 c = lds_read_tr16(vt + (cbase + 8) * 256 + ((g ^ vsw) << 4) + vhalf);
+            return half8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
+        };
 
-    // natural-unit max and the row sums (every element of lacc holds l)
-    float m_nat[kPRB], l_run[kPRB];
+        // Iteration i in two phases of explicitly ordered slots (each slot:
+        // the LDS reads it prefetches, then its vector work and MFMAs;
+        // nothing moves across slots):
+        // A: S(i + 1) = K(i + 1) Q^T on the matrix cores (eight slots of two
+        //    MFMAs, K operands read two slots ahead) while the vector ALU
+        //    turns S(i) into unnormalised probabilities p = exp2(s c - m c),
+        //    rounded to f16 (RNE) into the P^T operands; the first V
+        //    operands are read in the last slot.
+        // B: O^T += V(i)^T P(i)^T and the row sums of the f16 probabilities
+        //    (four slots of four MFMAs, V operands read one slot ahead).
+        // P^T operand kk holds cells 16 kk .. 16 kk + 15, i.e. registers
+        // 8 (kk & 1) .. + 7 of S^T block kk / 2.
+        auto body = [&](const int i, const bool qk, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
+            const float mc = m_run == -AL_INF ? 0.0f : m_run * cexp;
+            // the buffers' offsets as opaque values: otherwise the compiler
+            // keeps every buffer's read addresses live across the loop
+            int kb_ = kbuf(i + 1), vb_ = vbuf(i);
+            asm volatile("" : "+s"(kb_), "+s"(vb_));
+            half8 pf[4];
+            half8 kq[8][2];
+            half8 vc[4], vn[4];
+            if (qk) {
 #pragma unroll
-    for (int rb = 0; rb < kPRB; ++rb) {
-        m_nat[rb] = m_run[rb] == -AL_INF ? -AL_INF : m_run[rb] * (cexp / kLog2e);
-        l_run[rb] = lacc[rb][0];
+                for (int ks = 0; ks < 2; ++ks) {
+                    kq[ks][0] = k_read(kb_, 0, ks);
+                    kq[ks][1] = k_read(kb_, 1, ks);
+                }
+                nxt[0] = floatx16{};
+                nxt[1] = floatx16{};
+            }
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                if (qk && ks + 2 < 8) {
+                    kq[ks + 2][0] = k_read(kb_, 0, ks + 2);
+                    kq[ks + 2][1] = k_read(kb_, 1, ks + 2);
+                }
+                if (ks == 7) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) vc[db] = v_read(vb_, 0, db);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const int cb = ks >> 2, v0 = 4 * (ks & 3), kk = 2 * cb + (v0 >> 3), e0 = v0 & 4;
+#pragma unroll
+                for (int u = 0; u < 4; u += 2) {
+                    const float2v e = {__builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u], cexp, -mc)),
+                                      __builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u + 1], cexp, -mc))};
+                    half2v hv = __builtin_convertvector(e, half2v);
+                    asm volatile("" : "+v"(hv));          // keeps the exponentials in this slot
+                    pf[kk][e0 + u] = hv[0];
+                    pf[kk][e0 + u + 1] = hv[1];
+                }
+                if (qk) {
+                    nxt[0] = mfma32(kq[ks][0], qf[ks], nxt[0]);
+                    nxt[1] = mfma32(kq[ks][1], qf[ks], nxt[1]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            const half2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
+#pragma unroll
+            for (int kk = 0; kk < 4; ++kk) {
+                if (kk < 3) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) vn[db] = v_read(vb_, kk + 1, db);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int w = 0; w < 4; ++w)
+                    l_run = __builtin_amdgcn_fdot2(half2v{pf[kk][2 * w], pf[kk][2 * w + 1]}, one2, l_run, false);
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[db] = mfma32(vc[db], pf[kk], o[db]);
+                if (kk < 3) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db) vc[db] = vn[db];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        floatx16 s0[2], s1[2];
+        if (NI > 0) {
+            {
+                half8 kop[2][8];
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int ks = 0; ks < 8; ++ks) kop[cb][ks] = k_read(kbuf(0), cb, ks);
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb) {
+                    floatx16 acc = {};
+#pragma unroll
+                    for (int ks = 0; ks < 8; ++ks) acc = mfma32(kop[cb][ks], qf[ks], acc);
+                    s0[cb] = acc;
+                }
+                finish_scores(s0, tile_c0(0));
+            }
+            // iteration i: S(i) in s0 for even i, s1 for odd i
+            auto iteration = [&](const int i, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
+                __syncthreads();                  // (B_i) K(i + 1), V(i) landed; iteration i - 1 done
+                body(i, true, cur, nxt);
+                finish_scores(nxt, tile_c0(i + 1));
+            };
+            int i = 0;
+            for (; i + 2 < NI; i += 2) {
+                iteration(i, s0, s1);
+                iteration(i + 1, s1, s0);
+            }
+            if (i + 1 < NI) {
+                iteration(i, s0, s1);
+                ++i;
+            }
+            __syncthreads();                      // (B_{NI - 1}) V(NI - 1) landed
+            if (i & 1) body(i, false, s1, s0);
+            else body(i, false, s0, s1);
+        }
+        __syncthreads();                          // (3) rings free
+    }
+    float m_nat = m_run == -AL_INF ? -AL_INF : m_run * (cexp / kLog2e);
+    float l_row = pair_sum(l_run);
+
+    // The splits within the workgroup merge through LDS: split 1 stores its
+    // rows' state as a record [row][132], split 0 combines it with its own.
+    if constexpr (S::SP == 2) {
+        float * rec = (float *) lds + rr * kRowStride;
+        if (!producer && si == 1) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int bq = 0; bq < 4; ++bq)
+                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * h) =
+                        float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
+            if (h == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
+        }
+        __syncthreads();
+    }
+    const bool owner = !producer && si == 0;               // holds the workgroup's merged rows
+    if (S::SP == 2 && owner) {
+        const float * rec = (const float *) lds + rr * kRowStride;
+        const float2 ml = *(const float2 *) (rec + 128);
+        const float M = fmaxf(m_nat, ml.x);
+        const float Mu = M == -AL_INF ? 0.0f : M;
+        const float wa = exp_fast(m_nat - Mu), wb = exp_fast(ml.x - Mu);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int bq = 0; bq < 4; ++bq) {
+                const float4 x = *(const float4 *) (rec + 32 * db + 8 * bq + 4 * h);
+                o[db][4 * bq] = o[db][4 * bq] * wa + x.x * wb;
+                o[db][4 * bq + 1] = o[db][4 * bq + 1] * wa + x.y * wb;
+                o[db][4 * bq + 2] = o[db][4 * bq + 2] * wa + x.z * wb;
+                o[db][4 * bq + 3] = o[db][4 * bq + 3] * wa + x.w * wb;
+            }
+        l_row = l_row * wa + ml.y * wb;
+        m_nat = M;
     }
 
-    // Merge: every wave publishes its 32-row state to LDS [split][row][132]
-    // (the rings are free once all waves are past their loops), then the
-    // workgroup combines the 4 splits of each (row, 4 dims) and writes it.
-    __syncthreads();
-    float * recs = (float *) &lds[0];
-    {
-        float * rec = recs + cs * (kPRows * kRowStride);
+    // O^T lane l: row lr, dims 32 db + 8 bq + 4 h .. + 3 in o[db][4 bq .. 4 bq + 3].
+    // One workgroup per row tile: the owners put the finished rows into LDS
+    // (past the merge records; 16-byte granule g of row r at slot g ^ (r & 31)),
+    // then all threads store whole rows, 16 bytes per lane.
+    if (p.n_split == 1) {
+        float * stage = (float *) (lds + 80 * 1024);
+        if (owner && rvalid) {
+            const int hq = kvh * p.G + (row0 + rr) - tok_of(row0 + rr) * p.G;
+            const RowScale rs = row_scale(m_nat, l_row, p.sinks, hq);
 #pragma unroll
-        for (int rb = 0; rb < kPRB; ++rb) {
-            float * row = rec + (32 * rh + 16 * rb + n) * kRowStride;
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int d = 0; d < 8; ++d) *(float4 *) (row + 16 * d + 4 * g) = float4{o[rb][d][0], o[rb][d][1], o[rb][d][2], o[rb][d][3]};
-            if (g == 0) *(float2 *) (row + 128) = float2{m_nat[rb], l_run[rb]};
+                for (int bq = 0; bq < 4; ++bq) {
+                    const int g = 8 * db + 2 * bq + h;
+                    *(float4 *) (stage + rr * 128 + 4 * (g ^ (rr & 31))) =
+                        apply_scale(float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]}, rs);
+                }
         }
+        __syncthreads();
+        for (int item = threadIdx.x; item < rows_here * 32; item += 2 * kWaves * 64) {
+            const int r = item >> 5, g = item & 31;
+            const int rg_ = row0 + r;
+            const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
+            float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
+            *(float4 *) (out + 4 * g) = *(const float4 *) (stage + r * 128 + 4 * (g ^ (r & 31)));
+        }
+        return;
     }
+
+    // Workgroup splits: publish this workgroup's record [unit][sx][row][132]
+    // with device-coherent stores; the last workgroup of the row tile to
+    // arrive combines the records of all of them (fixed order) into dst.
+    const int unit = (b * p.Hkv + kvh) * p.n_row_tiles + rt;
+    constexpr uint32_t RS = ROWS * kRowStride * 4;                 // record bytes
+    const rsrc_t rec = make_rsrc(p.part + (int64_t) unit * p.n_split * (ROWS * kRowStride), RS * (uint32_t) p.n_split);
+    if (owner) {
+        const uint32_t row = (uint32_t) sx * RS + (uint32_t) (rr * kRowStride * 4);
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int bq = 0; bq < 4; ++bq)
+                buf_store16_dev(float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]}, rec,
+                                row + (uint32_t) ((32 * db + 8 * bq + 4 * h) * 4));
+        if (h == 0) buf_store8_dev(float2{m_nat, l_row}, rec, row + 128 * 4);
+    }
+    complete_wave_memops();
     __syncthreads();
+    unsigned * cnt = p.counters + unit;
+    int * s_last = (int *) (lds + kLds - 16);                       // past the merge rows
+    if (threadIdx.x == 0) *s_last = (add_agent(cnt, 1u) == (unsigned) (p.n_split - 1));
+    __syncthreads();
+    if (!*s_last) return;
+    order_after_counter();
+    if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
+    // thread t takes (row, 4 dims) items t, t + kMerge, ...: all records' loads in flight at once
+    for (int item = threadIdx.x; item < rows_here * 32; item += 2 * kWaves * 64) {
+        const int r = item >> 5, d4 = item & 31;
+        float2 ml[kMaxPrefillSplit];
+        float4 ov[kMaxPrefillSplit];
 #pragma unroll
-    for (int k = 0; k < kPRows * 32 / (kPW * 64); ++k) {
-        const int item = k * kPW * 64 + threadIdx.x;
-        const int rr = item >> 5, d4 = item & 31;
-        if (rr >= rows_here) continue;
-        float2 ml[kCS];
-        float M = -AL_INF;
-#pragma unroll
-        for (int c = 0; c < kCS; ++c) {
-            ml[c] = *(const float2 *) (recs + (c * kPRows + rr) * kRowStride + 128);
-            M = fmaxf(M, ml[c].x);
+        for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
+            const uint32_t row = (uint32_t) min(s2, p.n_split - 1) * RS + (uint32_t) (r * kRowStride * 4);
+            ml[s2] = buf_load8_dev(rec, row + 128 * 4);
+            ov[s2] = buf_load16_dev(rec, row + (uint32_t) (d4 * 16));
         }
-        const float Mu = (M == -AL_INF) ? 0.0f : M;
+        float M = ml[0].x;
+#pragma unroll
+        for (int s2 = 1; s2 < kMaxPrefillSplit; ++s2) M = s2 < p.n_split ? fmaxf(M, ml[s2].x) : M;
+        const float Mu = M == -AL_INF ? 0.0f : M;
         float L = 0.0f;
         float4 acc = {0, 0, 0, 0};
 #pragma unroll
-        for (int c = 0; c < kCS; ++c) {
-            const float w = exp_fast(ml[c].x - Mu);
-            L += w * ml[c].y;
-            const float4 x = *(const float4 *) (recs + (c * kPRows + rr) * kRowStride + 4 * d4);
-            acc.x += w * x.x; acc.y += w * x.y; acc.z += w * x.z; acc.w += w * x.w;
+        for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
+            const float w = s2 < p.n_split ? exp_fast(ml[s2].x - Mu) : 0.0f;
+            L += w * ml[s2].y;
+            acc.x += w * ov[s2].x; acc.y += w * ov[s2].y; acc.z += w * ov[s2].z; acc.w += w * ov[s2].w;
         }
-        const int tk = (row0 + rr) / p.G;
-        const int hq = kvh * p.G + (row0 + rr) % p.G;
+        const int rg_ = row0 + r;
+        const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
         float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
         *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
     }
@@ -478,9 +603,9 @@ __global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, i
     const uint16_t * row = (const uint16_t *) (p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3);
     int last0 = -1, first_inf = INT32_MAX, bad = 0;
     for (int c = threadIdx.x; c < p.n_kv; c += blockDim.x) {
-        const uint16_t h = row[c];
-        if ((h & 0x7fffu) == 0) last0 = c;
-        else if (h == 0xfc00u) first_inf = min(first_inf, c);
+        const uint16_t hb = row[c];
+        if ((hb & 0x7fffu) == 0) last0 = c;
+        else if (hb == 0xfc00u) first_inf = min(first_inf, c);
         else bad = 1;
     }
 #pragma unroll
@@ -518,9 +643,17 @@ hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int *
 
 size_t fattn_prefill_lds_bytes() { return (size_t) kLds; }
 
-hipError_t fattn_prefill_launch(const FattnParams & p, hipStream_t stream) {
-    const dim3 grid((unsigned) ((int64_t) p.Hkv * p.n_row_tiles * p.B));
-    if (p.softcap != 0.0f) hipLaunchKernelGGL(fattn_prefill_kernel<true>, grid, dim3(kPW * 64), 0, stream, p);
-    else                   hipLaunchKernelGGL(fattn_prefill_kernel<false>, grid, dim3(kPW * 64), 0, stream, p);
+hipError_t fattn_prefill_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream) {
+    if (p.n_split < 1 || p.n_split > kMaxPrefillSplit || (rows_per_tile != 64 && rows_per_tile != 128))
+        return hipErrorInvalidValue;
+    const dim3 grid((unsigned) p.Hkv, (unsigned) p.n_split, (unsigned) ((int64_t) p.n_row_tiles * p.B));
+    const bool sc = p.softcap != 0.0f;
+    if (rows_per_tile == 128) {
+        if (sc) hipLaunchKernelGGL((fattn_prefill_kernel<4, true>), grid, dim3(2 * kWaves * 64), 0, stream, p);
+        else    hipLaunchKernelGGL((fattn_prefill_kernel<4, false>), grid, dim3(2 * kWaves * 64), 0, stream, p);
+    } else {
+        if (sc) hipLaunchKernelGGL((fattn_prefill_kernel<2, true>), grid, dim3(2 * kWaves * 64), 0, stream, p);
+        else    hipLaunchKernelGGL((fattn_prefill_kernel<2, false>), grid, dim3(2 * kWaves * 64), 0, stream, p);
+    }
     return hipGetLastError();
 }

@@ -1,0 +1,44 @@
+// Pieces shared by the prefill kernels (fattn_prefill.hip: 128-row tiles,
+// fattn_prefill_w64.hip: 64-row tiles), which are compiled with different
+// register-allocation options.
+#pragma once
+
+#include "fattn_tile.hpp"
+
+namespace fattn_prefill {
+
+using namespace fattn;
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float float2v __attribute__((ext_vector_type(2)));
+
+constexpr int kWaves = 4;                        // one per SIMD, 32 rows each
+constexpr int kLds = 160 * 1024;                 // the rings of all splits (all of a CU's LDS)
+constexpr int kMaxPrefillSplit = kFattnPrefillMaxSplit;
+constexpr float kLog2e = 1.44269504088896341f;
+
+__device__ __forceinline__ floatx16 mfma32(half8 a, half8 b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Values of lanes l % 32 and l % 32 + 32 (the two lanes holding one row).
+__device__ __forceinline__ float pair_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int) r[0]), __builtin_bit_cast(float, (int) r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return __builtin_bit_cast(float, (int) r[0]) + __builtin_bit_cast(float, (int) r[1]);
+}
+
+// Waits until at most N LDS-DMA / vector memory instructions of this wave are
+// outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    mem_barrier();
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(N));
+    mem_barrier();
+}
+
+}  // namespace fattn_prefill

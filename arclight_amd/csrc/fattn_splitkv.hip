@@ -204,12 +204,13 @@ __global__ __launch_bounds__(W * 64) void fattn_splitkv_kernel(const FattnParams
             for (int rb = 0; rb < RB; ++rb) {
                 if (!rvalid[rb]) continue;
                 float * out = (float *) (p.dst + ((int64_t) (b * p.T + tok[rb]) * p.Hq + head[rb]) * p.dst_nb1);
+                const RowScale rs = row_scale(m_run[rb], l_run[rb], p.sinks, head[rb]);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float4 lo = {o[rb][0][i], o[rb][1][i], o[rb][2][i], o[rb][3][i]};
                     const float4 hi4 = {o[rb][4][i], o[rb][5][i], o[rb][6][i], o[rb][7][i]};
-                    *(float4 *) (out + 32 * g + 8 * i) = finalize4(lo, m_run[rb], l_run[rb], p.sinks, head[rb]);
-                    *(float4 *) (out + 32 * g + 8 * i + 4) = finalize4(hi4, m_run[rb], l_run[rb], p.sinks, head[rb]);
+                    *(float4 *) (out + 32 * g + 8 * i) = apply_scale(lo, rs);
+                    *(float4 *) (out + 32 * g + 8 * i + 4) = apply_scale(hi4, rs);
                 }
             }
         }

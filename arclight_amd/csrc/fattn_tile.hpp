@@ -159,6 +159,30 @@ __device__ __forceinline__ void publish_state(const rsrc_t rr, uint32_t rec_off,
 }
 
 // Sinks (arm.cpp:2402-2416) and 1/S (arm.cpp:2419-2420) on one 4-dim group.
+// The same finalisation split into a per-row part (once per row) and a
+// per-value part: o_out = (o * ms) * inv, ms = 1 unless a sink outweighs M.
+struct RowScale {
+    float ms, inv;
+};
+__device__ __forceinline__ RowScale row_scale(float M, float L, const float * sinks, int head) {
+    float ms = 1.0f;
+    if (sinks) {
+        const float s = sinks[head];
+        if (s > M) {
+            ms = expf(M - s);
+            L = L * ms + 1.0f;
+        } else {
+            L = L + expf(s - M);
+        }
+    }
+    return RowScale{ms, 1.0f / L};
+}
+__device__ __forceinline__ float4 apply_scale(float4 o, const RowScale r) {
+    o.x *= r.ms; o.y *= r.ms; o.z *= r.ms; o.w *= r.ms;
+    o.x *= r.inv; o.y *= r.inv; o.z *= r.inv; o.w *= r.inv;
+    return o;
+}
+
 __device__ __forceinline__ float4 finalize4(float4 o, float M, float L, const float * sinks, int head) {
     if (sinks) {
         const float s = sinks[head];
