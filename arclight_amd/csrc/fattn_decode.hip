@@ -9,7 +9,8 @@
 // blocks sharing every K/V operand read (speculative verify). Its WS wavefronts take the
 // range's 16-cell stages in turn (wave ws: stages ws, ws + WS, ...), each
 // with a private ring of NB LDS stage buffers, so the waves never wait for
-// each other until the end. The 1-D grid runs split fastest.
+// each other until the end. The grid (split, kv head, stream) runs split
+// fastest.
 //
 // Memory path. A stage is the head's 16 K rows and 16 V rows (4 KiB each),
 // moved by LDS-DMA buffer loads of 1 KiB per instruction (4 cells x 256 B),
@@ -68,14 +69,14 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const int g = lane >> 4;
     const int n = lane & 15;
 
-    int id = blockIdx.x;
-    const int split = id % p.n_split;
-    id /= p.n_split;
-    const int kvh = id % p.Hkv;
-    const int b = id / p.Hkv;
+    // grid (split, kv head, stream): no integer division on the way to the
+    // first loads
+    const int split = blockIdx.x;
+    const int kvh = blockIdx.y;
+    const int b = blockIdx.z;
     const int unit = b * p.Hkv + kvh;
     const int rows_here = min(16 * RB, p.R);
-    const int t_last = (rows_here - 1) / p.G;
+    const int t_last = div_g(rows_here - 1, p.G, p.g_magic);
 
     // lengths: fixed at launch, or read now (a graph replayed per decode step)
     int hi = p.kv_hi;
@@ -97,8 +98,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 
     // K/V rows of this stream and head (loads past the end read 0)
     const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
-    const char * kbase = p.k + (int64_t) (b / p.rk3) * p.k_nb3 + (int64_t) kvh * p.k_nb2;
-    const char * vbase = p.v + (int64_t) (b / p.rv3) * p.v_nb3 + (int64_t) kvh * p.v_nb2;
+    const int bk = p.rk3 == 1 ? b : b / p.rk3, bv = p.rv3 == 1 ? b : b / p.rv3;
+    const char * kbase = p.k + (int64_t) bk * p.k_nb3 + (int64_t) kvh * p.k_nb2;
+    const char * vbase = p.v + (int64_t) bv * p.v_nb3 + (int64_t) kvh * p.v_nb2;
     const int4v kd = raw_desc(kbase, (uint32_t) (p.n_kv - 1) * k_nb1 + 256);
     const int4v vd = raw_desc(vbase, (uint32_t) (p.n_kv - 1) * v_nb1 + 256);
 
@@ -119,8 +121,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     for (int rb = 0; rb < RB; ++rb) {
         const int r = 16 * rb + n;
         rvalid[rb] = r < rows_here;
-        tok[rb] = rvalid[rb] ? r / p.G : 0;
-        head[rb] = kvh * p.G + (rvalid[rb] ? r % p.G : 0);
+        const int t = div_g(rvalid[rb] ? r : 0, p.G, p.g_magic);
+        tok[rb] = t;
+        head[rb] = kvh * p.G + (rvalid[rb] ? r - t * p.G : 0);
     }
 
     // Mask rows (f16, cells along a row) also travel by DMA, one 1 KiB block
@@ -133,8 +136,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     if constexpr (HAS_MASK) {
         md = raw_desc(p.mask + (int64_t) (b % p.m_ne3) * p.m_nb3, p.m_slice_bytes);
         const int mrow = (lane >> 1) & (16 * RB - 1);
-        const int mt_ = mrow < rows_here ? mrow / p.G : 0;
-        const int mh = kvh * p.G + (mrow < rows_here ? mrow % p.G : 0);
+        const int mr = mrow < rows_here ? mrow : 0;
+        const int mt_ = div_g(mr, p.G, p.g_magic);
+        const int mh = kvh * p.G + mr - mt_ * p.G;
         msrc = (uint32_t) ((int64_t) mt_ * p.m_nb1 + (int64_t) (mh % p.m_ne2) * p.m_nb2) + (uint32_t) ((lane & 1) * 16);
     }
 
@@ -162,7 +166,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         const int4v qd = raw_desc(p.q + (int64_t) b * p.q_nb3, p.q_bytes);
         for (int i = ws, r2 = rr; i < (rows_here + 1) / 2; i += WS, r2 += 2 * WS) {
             const int rq = r2 < rows_here ? r2 : 0;
-            const uint32_t qofs = (uint32_t) ((rq / p.G) * p.q_nb1 + (kvh * p.G + rq % p.G) * p.q_nb2);
+            const int tq = div_g(rq, p.G, p.g_magic);
+            const uint32_t qofs = (uint32_t) (tq * p.q_nb1 + (kvh * p.G + rq - tq * p.G) * p.q_nb2);
             dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r2 & 15))) & 31) * 16, lds_addr(qlds) + (uint32_t) (i * 1024));
         }
     }
@@ -475,8 +480,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             if (half == 0 && idx < n_items) {
                 const float L = Lh + Lo;
                 const float4 acc = {ah.x + ao.x, ah.y + ao.y, ah.z + ao.z, ah.w + ao.w};
-                const int t = rr / p.G;
-                const int hq = kvh * p.G + rr % p.G;
+                const int t = div_g(rr, p.G, p.g_magic);
+                const int hq = kvh * p.G + rr - t * p.G;
                 float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
                 *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
             }
@@ -486,7 +491,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 
 template <int WS, int NB>
 hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
-    const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
+    const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
     if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true, 1>), grid, dim3(WS * 64), 0, stream, p);
     else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1>), grid, dim3(WS * 64), 0, stream, p);
     return hipGetLastError();
@@ -509,7 +514,7 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
     if (p.R > 16) {
         // 17..32 rows: two row blocks, 8 waves x 2 stages
         if (p.R > 32 || waves != 8 || stages != 2) return hipErrorInvalidValue;
-        const dim3 grid((unsigned) ((int64_t) p.n_split * p.Hkv * p.B));
+        const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
         if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, true, 2>), grid, dim3(8 * 64), 0, stream, p);
         else        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2>), grid, dim3(8 * 64), 0, stream, p);
         return hipGetLastError();

@@ -324,7 +324,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // the wave does not wholly see, and the reference max moved when the
         // tile outgrows it (a rare, uniform branch; the first visible tile
         // always does)
-        auto finish_scores = [&](floatx16 (&sc)[2], const int c0) {
+        auto prepare = [&](floatx16 (&sc)[2], const int c0) {
             if constexpr (SOFTCAP) {
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
@@ -340,6 +340,11 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                         sc[cb][v] = c <= lim ? sc[cb][v] : -AL_INF;
                     }
             }
+        };
+        // fresh scores ready: the reference max moved when the tile outgrows
+        // it (a rare, uniform branch; the first visible tile always does)
+        auto finish_scores = [&](floatx16 (&sc)[2], const int c0) {
+            prepare(sc, c0);
             if (__any(lane_max(sc) > m_run + tau)) rescale(sc);
         };
         auto k_read = [&](const int kbo, const int cb, const int ks) {
@@ -367,6 +372,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         //    (four slots of four MFMAs, V operands read one slot ahead).
         // P^T operand kk holds cells 16 kk .. 16 kk + 15, i.e. registers
         // 8 (kk & 1) .. + 7 of S^T block kk / 2.
+        float mx;                                 // lane max of S(i + 1), from body(i)
         auto body = [&](const int i, const bool qk, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
             const float mc = m_run == -AL_INF ? 0.0f : m_run * cexp;
             // the buffers' offsets as opaque values: otherwise the compiler
@@ -412,12 +418,25 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            if (qk) prepare(nxt, tile_c0(i + 1));
+            // the lane max of S(i + 1) in the slots of phase B (from slot 1
+            // on, when the last QK^T results are ready)
+            float mx0 = -AL_INF, mx1 = -AL_INF;
             const half2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) {
                 if (kk < 3) {
 #pragma unroll
                     for (int db = 0; db < 4; ++db) vn[db] = v_read(vb_, kk + 1, db);
+                }
+                if (qk && kk > 0 && kk < 3) {             // slot 1: block 0, slot 2: block 1
+                    const floatx16 & x = nxt[kk - 1];
+                    float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
+#pragma unroll
+                    for (int v = 3; v < 15; v += 2) m = fmaxf(fmaxf(m, x[v]), x[v + 1]);
+                    m = fmaxf(m, x[15]);
+                    if (kk == 1) mx0 = m;
+                    else mx1 = m;
                 }
                 __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -431,6 +450,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
+            mx = fmaxf(mx0, mx1);
         };
 
         floatx16 s0[2], s1[2];
@@ -454,7 +474,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             auto iteration = [&](const int i, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
                 __syncthreads();                  // (B_i) K(i + 1), V(i) landed; iteration i - 1 done
                 body(i, true, cur, nxt);
-                finish_scores(nxt, tile_c0(i + 1));
+                if (__any(mx > m_run + tau)) rescale(nxt);
             };
             int i = 0;
             for (; i + 2 < NI; i += 2) {

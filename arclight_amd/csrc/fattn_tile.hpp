@@ -159,6 +159,13 @@ __device__ __forceinline__ void publish_state(const rsrc_t rr, uint32_t rec_off,
 }
 
 // Sinks (arm.cpp:2402-2416) and 1/S (arm.cpp:2419-2420) on one 4-dim group.
+// r / G for the row index r of a kv-head group: a multiply-high by
+// magic = ceil(2^32 / G) (exact for r G < 2^32, which the plan checks), or r
+// itself for G = 1.
+__device__ __forceinline__ int div_g(const int r, const int G, const uint32_t magic) {
+    return G == 1 ? r : (int) __umulhi((uint32_t) r, magic);
+}
+
 // The same finalisation split into a per-row part (once per row) and a
 // per-value part: o_out = (o * ms) * inv, ms = 1 unless a sink outweighs M.
 struct RowScale {
