@@ -474,7 +474,9 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         pl.counters_bytes = kFattnCounterBytes;
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
     }
-    if (m.data && prefill_shape) {
+    // the mask pass reads mask rows 16 bytes at a time
+    const bool mask_rows16 = m.data && aligned16(m.data) && m.nb[1] % 16 == 0 && m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0;
+    if (m.data && prefill_shape && mask_rows16) {
         // the gate lives in the counter region, which is reserved also when
         // the split-KV plan has a single split; the prefill kernel and the
         // split-KV kernel share the counters and the records (only one of

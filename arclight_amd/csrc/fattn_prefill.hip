@@ -614,40 +614,52 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     }
 }
 
-// One workgroup per mask row (token t of mask slice (i2, i3)) over cells
-// [0, n_kv): the last cell holding +-0 (-1 if none) into lims, and 1 into
-// gate[0] when the row is not a run of zeros followed by -inf (another
-// value, or a zero after a -inf).
+// One wavefront per mask row (token t of mask slice (i2, i3)), four rows
+// per workgroup, over cells [0, n_kv): the last cell holding +-0 (-1 if
+// none) into lims, and 1 into gate[0] when the row is not a run of zeros
+// followed by -inf (another value, or a zero after a -inf). Rows are read
+// 16 bytes (8 cells) per lane and load; the plan requires 16-byte aligned
+// mask rows.
 __global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, int32_t * lims, int * gate) {
-    const int t = blockIdx.x, i2 = blockIdx.y, i3 = blockIdx.z;
-    const uint16_t * row = (const uint16_t *) (p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3);
+    const int lane = threadIdx.x & 63;
+    const int t = 4 * blockIdx.x + (threadIdx.x >> 6), i2 = blockIdx.y, i3 = blockIdx.z;
+    if (t >= p.T) return;
+    const char * rowp = p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3;
     int last0 = -1, first_inf = INT32_MAX, bad = 0;
-    for (int c = threadIdx.x; c < p.n_kv; c += blockDim.x) {
-        const uint16_t hb = row[c];
-        if ((hb & 0x7fffu) == 0) last0 = c;
+    auto classify = [&](const uint32_t hb, const int c) {
+        if ((hb & 0x7fffu) == 0) last0 = max(last0, c);
         else if (hb == 0xfc00u) first_inf = min(first_inf, c);
         else bad = 1;
+    };
+    // eight 16-byte loads per lane in flight at once (4096 cells per round)
+    const int n8 = p.n_kv >> 3;
+    for (int j0 = 0; j0 < n8; j0 += 8 * 64) {
+        uint4 w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + 64 * u + lane;
+            w[u] = j < n8 ? *(const uint4 *) (rowp + 16 * (int64_t) j) : uint4{0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + 64 * u + lane;
+            if (j >= n8) continue;
+            const uint32_t x[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                classify(x[e] & 0xffffu, 8 * j + 2 * e);
+                classify(x[e] >> 16, 8 * j + 2 * e + 1);
+            }
+        }
     }
+    for (int c = 8 * n8 + lane; c < p.n_kv; c += 64) classify(((const uint16_t *) rowp)[c], c);
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) {
         last0 = max(last0, __shfl_xor(last0, off));
         first_inf = min(first_inf, __shfl_xor(first_inf, off));
         bad |= __shfl_xor(bad, off);
     }
-    __shared__ int s[3][4];
-    const int w = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        s[0][w] = last0;
-        s[1][w] = first_inf;
-        s[2][w] = bad;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int i = 1; i < (int) (blockDim.x >> 6); ++i) {
-            last0 = max(last0, s[0][i]);
-            first_inf = min(first_inf, s[1][i]);
-            bad |= s[2][i];
-        }
+    if (lane == 0) {
         lims[((int64_t) i3 * p.m_ne2 + i2) * p.T + t] = last0;
         if (bad || last0 > first_inf) __hip_atomic_store(gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -656,7 +668,7 @@ __global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, i
 }  // namespace
 
 hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream) {
-    const dim3 grid((unsigned) p.T, (unsigned) p.m_ne2, (unsigned) p.m_ne3);
+    const dim3 grid((unsigned) ((p.T + 3) / 4), (unsigned) p.m_ne2, (unsigned) p.m_ne3);
     hipLaunchKernelGGL(mask_limits_kernel, grid, dim3(256), 0, stream, p, lims, gate);
     return hipGetLastError();
 }

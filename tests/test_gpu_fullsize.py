@@ -1,6 +1,7 @@
 """Parity at the benchmark shapes themselves: Qwen3-8B-shape speculative
 verify over an 8192-cell context, Qwen3-32B-shape decode at 32768 cells and
-prefill in 1024-token causal chunks, plus a size-independent property of
+prefill in 1024-token causal chunks, Qwen3-4B-shape prefill in 256-token
+ubatches (implicit and explicit masks), plus a size-independent property of
 the full 2048-token Qwen3-4B prefill: its four causal chunks of 512 equal
 one causal call over all 2048 tokens.
 
@@ -108,3 +109,22 @@ def test_prefill_explicit_mask_on_the_prefill_kernel(gpu):
     m3 = O.causal_mask(512, n_kv, 0, kv_len=512)
     _case("prefill first chunk, explicit causal mask")
     assert_parity(run_gpu(q, k, v, m3, scale=SCALE), O.attention(q, k, v, m3, scale=SCALE), what="first chunk mask")
+
+
+@pytest.mark.parametrize("pos0", [0, 1024, 1792])
+def test_prefill_qwen3_4b_ubatch256(gpu, pos0):
+    # ArcLight's default 256-token ubatch (apps/al-gen.cpp:129-130) at the
+    # Qwen3-4B shape: 8 ubatches make a 2048-token prompt; 1024 rows per kv
+    # head take the prefill kernel's 64-row tiles, with workgroup splits.
+    # Whole output against the oracle, implicit masking and the explicit f16
+    # mask without length hints (the call as nnml makes it).
+    T, kv_len = 256, pos0 + 256
+    n_kv = 2048
+    q, k, v = O.make_inputs(256 + pos0, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=kv_len, causal_pos0=pos0)
+    _case(f"prefill Qwen3-4B ubatch 256 pos0 {pos0} implicit")
+    assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=kv_len, causal_pos0=pos0), ref,
+                  what=f"ubatch 256 pos0 {pos0} implicit")
+    _case(f"prefill Qwen3-4B ubatch 256 pos0 {pos0} explicit mask")
+    got = run_gpu(q, k, v, O.causal_mask(T, n_kv, pos0, kv_len=kv_len), scale=SCALE)
+    assert_parity(got, ref, what=f"ubatch 256 pos0 {pos0} explicit")
