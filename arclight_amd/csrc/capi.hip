@@ -169,13 +169,6 @@ struct Plan {
     int rows_per_tile = 16;
     size_t counters_bytes = 0;
     size_t part_bytes = 0;
-    // split-KV plan of a many-row call with a mask tensor, gated behind the
-    // mask pass and the prefill kernel (FattnParams::row_lim)
-    bool masked_prefill = false;
-    int32_t prefill_tiles = 0;
-    int32_t prefill_split = 1;
-    int prefill_rows = kFattnPrefillRows;
-    size_t lims_bytes = 0;
 };
 
 bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
@@ -372,16 +365,18 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
                cell_tiles >= 2 * in_wg_split * (prefill_split + 1))
             ++prefill_split;
     }
-    const bool prefill_shape = !p.dyn && p.R >= prefill_min_rows() && prefill_units <= kFattnGateWord &&
+    // (an explicit mask: the prefill kernel reads its rows 16 bytes at a time)
+    const bool mask_rows16 = !m.data || (aligned16(m.data) && m.nb[1] % 16 == 0 && m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
+    const bool prefill_shape = !p.dyn && p.R >= prefill_min_rows() && prefill_units <= kFattnCounterWords &&
                                (uint64_t) p.R * (uint64_t) p.G < (1ull << 32) && prefill_tiles * B <= 65535 &&
                                (uint64_t) (n_kv + 64) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
-                               (uint64_t) (n_kv + 64) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
+                               (uint64_t) (n_kv + 64) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX && mask_rows16 &&
                                lds_per_block >= (int64_t) fattn_prefill_lds_bytes() && q_slice < INT32_MAX &&
                                (p.softcap != 0.0f || p.scale > 0.0f) && prefer_prefill();
     const size_t prefill_part = prefill_split > 1 ? (size_t) prefill_units * prefill_split * prefill_rows *
                                                         kFattnRecordStride * sizeof(float)
                                                   : 0;
-    if (!m.data && prefill_shape) {
+    if (prefill_shape) {
         pl.kernel = kPrefill;
         pl.rows_per_tile = prefill_rows;
         p.n_row_tiles = (int32_t) prefill_tiles;
@@ -417,7 +412,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     if (p.R <= 32 && prefer_decode() && (size_t) lds_per_block >= decode_lds + decode_q_lds &&
         mask_ok &&
         q_slice < INT32_MAX &&
-        decode_units <= kFattnGateWord &&
+        decode_units <= kFattnCounterWords &&
         (uint64_t) (n_kv + 16) * k.nb[1] + 256 <= (uint64_t) UINT32_MAX &&
         (uint64_t) (n_kv + 16) * v.nb[1] + 256 <= (uint64_t) UINT32_MAX) {
         pl.kernel = kDecode;
@@ -467,27 +462,12 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     int64_t cps_tiles = std::max<int64_t>(1, (tiles + n_split - 1) / n_split);
     p.cells_per_split = (int32_t) (cps_tiles * 32);
     n_split = std::max<int64_t>(1, (extent + p.cells_per_split - 1) / p.cells_per_split);
-    if (units > kFattnGateWord) n_split = 1;
+    if (units > kFattnCounterWords) n_split = 1;
     if (n_split == 1) p.cells_per_split = (int32_t) std::max<int64_t>(32, (extent + 31) / 32 * 32);
     p.n_split = (int32_t) n_split;
     if (p.n_split > 1) {
         pl.counters_bytes = kFattnCounterBytes;
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
-    }
-    // the mask pass reads mask rows 16 bytes at a time
-    const bool mask_rows16 = m.data && aligned16(m.data) && m.nb[1] % 16 == 0 && m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0;
-    if (m.data && prefill_shape && mask_rows16) {
-        // the gate lives in the counter region, which is reserved also when
-        // the split-KV plan has a single split; the prefill kernel and the
-        // split-KV kernel share the counters and the records (only one of
-        // them runs past its gate)
-        pl.masked_prefill = true;
-        pl.prefill_tiles = (int32_t) prefill_tiles;
-        pl.prefill_split = (int32_t) prefill_split;
-        pl.prefill_rows = prefill_rows;
-        pl.counters_bytes = kFattnCounterBytes;
-        pl.part_bytes = std::max(pl.part_bytes, prefill_part);
-        pl.lims_bytes = ((size_t) T * p.m_ne2 * p.m_ne3 * sizeof(int32_t) + 255) / 256 * 256;
     }
     *out = pl;
     return AL_OK;
@@ -500,7 +480,7 @@ extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
     if (al_device_cu_count(&n_cu) != AL_OK || al_device_lds_per_block(&lds) != AL_OK) return 0;
     Plan pl;
     if (make_plan(a, n_cu, lds, &pl) != AL_OK) return 0;
-    return pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
+    return pl.counters_bytes + pl.part_bytes;
 }
 
 // One call with the plan's workspace: the caller's, else the library's for
@@ -514,8 +494,7 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
     Plan pl;
     rc = make_plan(a, n_cu, lds, &pl);
     if (rc != AL_OK) return rc;
-    const size_t need = pl.counters_bytes + pl.part_bytes + pl.lims_bytes;
-    int32_t * lims = nullptr;
+    const size_t need = pl.counters_bytes + pl.part_bytes;
     if (need) {
         void * ws = noalloc_ws ? noalloc_ws : a->workspace;
         if (noalloc_ws) {
@@ -532,30 +511,10 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
         }
         pl.p.counters = (unsigned *) ws;
         pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
-        lims = (int32_t *) ((char *) ws + pl.counters_bytes + pl.part_bytes);
     }
     rc = al_device_error_flag(&pl.p.err);
     if (rc != AL_OK) return rc;
     hipError_t e;
-    if (pl.masked_prefill) {
-        // the mask pass, then the prefill kernel on the mask's row limits and
-        // the split-KV kernel; the pass leaves exactly one of them running,
-        // and the split-KV kernel clears the gate for the next call
-        int * gate = (int *) pl.p.counters + kFattnGateWord;
-        hipStream_t st = (hipStream_t) a->stream;
-        FattnParams pp = pl.p;
-        pp.n_row_tiles = pl.prefill_tiles;
-        pp.n_split = pl.prefill_split;
-        pp.cells_per_split = 0;
-        pp.row_lim = lims;
-        pp.gate = gate;
-        e = fattn_mask_limits_launch(pl.p, lims, gate, st);
-        if (e == hipSuccess) e = fattn_prefill_launch(pp, pl.prefill_rows, st);
-        pl.p.gate = gate;
-        if (e == hipSuccess) e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, st);
-        if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
-        return AL_OK;
-    }
     switch (pl.kernel) {
         case kPrefill: e = fattn_prefill_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
         case kDecode:  e = fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream); break;
@@ -581,8 +540,8 @@ extern "C" int al_fattn_f16_worker(const al_fattn_args * a, int ith, int nth) {
 // no-allocation entry point
 // ---------------------------------------------------------------------------
 
-// The scratch of al_fattn_f16_noalloc: arrival counters and gate, merge
-// records and row limits, laid out as a caller workspace. One copy per GPU,
+// The scratch of al_fattn_f16_noalloc: arrival counters and merge records,
+// laid out as a caller workspace. One copy per GPU,
 // held until the process ends; every call on that GPU shares it.
 static __device__ __align__(256) unsigned char scratch[AL_FATTN_NOALLOC_SCRATCH_BYTES];
 

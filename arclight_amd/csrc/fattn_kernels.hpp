@@ -36,15 +36,6 @@ struct FattnParams {
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
     int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
     const int32_t * dyn;            // decode kernel: device {kv_len, causal_pos0} read at run time, or null
-    // Many-row calls with a mask tensor: the mask pass writes each mask
-    // row's last visible cell to row_lim ([m_ne3][m_ne2][T]) and sets
-    // gate[0] when some row is not a run of zeros followed by -inf; the
-    // prefill kernel then returns at once and the split-KV kernel, which
-    // otherwise returns at once, takes the call. gate[1] counts the split-KV
-    // workgroups that have read gate[0]; the last one clears both, so each
-    // call starts from a clear gate (also on a replayed graph).
-    const int32_t * row_lim;
-    int * gate;
 };
 
 // Split-KV kernel: rows per tile for R query rows per kv head (16, 32 or 64).
@@ -57,11 +48,11 @@ hipError_t fattn_splitkv_launch(const FattnParams & p, int rows_per_tile, hipStr
 // two cell splits within the workgroup), n_split workgroups per (kv head,
 // row tile, stream) (1..kFattnPrefillMaxSplit; with more than one, merge
 // records of rows_per_tile rows and arrival counters in the workspace);
-// needs fattn_prefill_lds_bytes() of LDS. Masking is the implicit
-// length / causal rule, optionally narrowed per row by the row limits that
-// the mask pass (fattn_mask_limits_launch) derives from a mask tensor.
+// needs fattn_prefill_lds_bytes() of LDS. Masking: the length / causal rule
+// and an explicit mask tensor (rows 16-byte aligned), whose rows the kernel
+// scans for their visible extent; a mask that is not a run of zeros then
+// -inf in every row of a tile is applied value by value in that tile.
 hipError_t fattn_prefill_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream);
-hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream);
 size_t fattn_prefill_lds_bytes();
 constexpr int kFattnPrefillRows = 128;          // query rows per workgroup (at most)
 constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row tile
@@ -79,10 +70,8 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
 constexpr int kFattnRecordStride = 132;
 // At most kFattnMaxSplit splits per row tile; one merge level.
 constexpr int kFattnMaxSplit = 32;
-// Every workspace starts with a fixed arrival-counter region, so that no
-// call's merge records ever overlap another call's counters; kernels leave
-// it zeroed. Its last two words are the gate of masked many-row calls
-// (FattnParams::gate), so at most kFattnGateWord counters precede them.
-// Records follow the region, then a masked call's row limits.
+// Every workspace starts with a fixed arrival-counter region (one counter
+// per row tile or kv head), so that no call's merge records ever overlap
+// another call's counters; kernels leave it zeroed. Records follow it.
 constexpr size_t kFattnCounterBytes = 256u << 10;
-constexpr int kFattnGateWord = (int) (kFattnCounterBytes / 4) - 2;
+constexpr int kFattnCounterWords = (int) (kFattnCounterBytes / 4);

@@ -1,6 +1,8 @@
 // Prefill (and long speculative-verify) attention for gfx950: many query rows
 // per kv head, masking given by the length / causal rule (kv_len,
-// causal_pos0) and optionally narrowed per row by the mask pass's row limits.
+// causal_pos0) and by an explicit f16 mask tensor: a mask whose rows are
+// runs of zeros followed by -inf becomes per-row extents, any other is
+// added value by value.
 // Semantics as nnml_compute_forward_flash_attn_ext_f16
 // (nnml/src/ops/arm/arm.cpp:2196-2433), numerics as fattn_splitkv.hip.
 //
@@ -98,7 +100,7 @@ __device__ __forceinline__ int4v uniform_desc(const char * base, const uint32_t 
                  __builtin_amdgcn_readfirstlane((int) bytes), 0x00020000};
 }
 
-template <int RG, bool SOFTCAP>
+template <int RG, bool SOFTCAP, bool MASK>
 __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const FattnParams p) {
     using S = Shape<RG>;
     constexpr int ROWS = S::ROWS, NK = S::NK, NV = S::NV, PER = S::PER;
@@ -133,17 +135,89 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     // row r of the kv head: token r / G, head kvh G + r % G
     auto tok_of = [&](const int r) { return p.G == 1 ? r : (int) __umulhi((uint32_t) r, p.g_magic); };
 
+    // An explicit mask (f16 rows of n_kv cells, 16-byte aligned) is read
+    // here first: every mask row that the tile's rows use (one per token
+    // when the mask is shared by the heads, else one per row) is scanned by
+    // one wavefront, 16 bytes per lane and load, for its last cell that is
+    // not -inf (the row's visible extent) and for whether it is a run of
+    // zeros followed by -inf. When every row is, the mask is exactly the
+    // extent and the tiles run as with the length rule; otherwise the whole
+    // workgroup adds slope * mask to its scores tile by tile (general mode).
+    // The results sit in a V buffer that no tile uses before the loop.
+    constexpr bool has_mask = MASK;           // the launch picks MASK = (p.mask != nullptr)
+    const int t0 = tok_of(row0);
+    const int n_units = !has_mask ? 0 : p.m_ne2 == 1 ? tok_of(row0 + rows_here - 1) - t0 + 1 : rows_here;
+    int * mtab = (int *) (lds + (RG == 4 ? NK + NV - 1 : NK + NV - 1) * kTileBytes);   // V buffer NV - 1 of split 0
+    auto mask_row = [&](const int r) {                    // mask row of tile row r (global row row0 + r)
+        const int rg_ = row0 + r, tok = tok_of(rg_);
+        const int hq = kvh * p.G + (rg_ - tok * p.G);
+        return p.mask + (int64_t) tok * p.m_nb1 + (int64_t) (p.m_ne2 == 1 ? 0 : hq % p.m_ne2) * p.m_nb2 +
+               (int64_t) (p.m_ne3 == 1 ? 0 : b % p.m_ne3) * p.m_nb3;
+    };
+    if constexpr (has_mask) {
+        for (int u = wave; u < n_units; u += 2 * kWaves) {
+            const int r_u = p.m_ne2 == 1 ? max(0, (t0 + u) * p.G - row0) : u;   // a tile row of the unit
+            const char * rowp = mask_row(r_u);
+            int last_fin = -1, last0 = -1, first_inf = INT32_MAX, bad = 0;
+            auto classify = [&](const uint32_t hb, const int c) {
+                if (hb != 0xfc00u) last_fin = max(last_fin, c);
+                if ((hb & 0x7fffu) == 0) last0 = max(last0, c);
+                else if (hb == 0xfc00u) first_inf = min(first_inf, c);
+                else bad = 1;
+            };
+            const int n8 = p.n_kv >> 3;
+            for (int j0 = 0; j0 < n8; j0 += 8 * 64) {
+                uint4 w[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int j = j0 + 64 * q + lane;
+                    w[q] = j < n8 ? *(const uint4 *) (rowp + 16 * (int64_t) j)
+                                  : uint4{0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u};
+                }
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int j = j0 + 64 * q + lane;
+                    if (j >= n8) continue;
+                    const uint32_t x[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        classify(x[e] & 0xffffu, 8 * j + 2 * e);
+                        classify(x[e] >> 16, 8 * j + 2 * e + 1);
+                    }
+                }
+            }
+            for (int c = 8 * n8 + lane; c < p.n_kv; c += 64) classify(((const uint16_t *) rowp)[c], c);
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                last_fin = max(last_fin, __shfl_xor(last_fin, off));
+                last0 = max(last0, __shfl_xor(last0, off));
+                first_inf = min(first_inf, __shfl_xor(first_inf, off));
+                bad |= __shfl_xor(bad, off);
+            }
+            if (lane == 0) {
+                const bool simple = !bad && last0 < first_inf;
+                mtab[2 * u] = simple ? last0 : last_fin;
+                mtab[2 * u + 1] = simple ? 0 : 1;
+            }
+        }
+        __syncthreads();                          // (0) the mask table
+    }
+    auto unit_of = [&](const int r) { return p.m_ne2 == 1 ? tok_of(row0 + r) - t0 : r; };
+    // general mode: some row of the tile is not a run of zeros then -inf
+    int general = 0;
+    if constexpr (has_mask) {
+        for (int u = lane; u < n_units; u += 64) general |= mtab[2 * u + 1];
+        general = __any(general) ? 1 : 0;
+    }
+
     // Last visible cell of a row: the length / causal rule, narrowed by the
-    // mask pass's row limits when a mask tensor came with the call.
+    // explicit mask's extent when a mask tensor came with the call.
     auto row_lim = [&](const int rr) {                    // rr: row within the tile, < rows_here
         const int r = row0 + rr;
         const int tok = tok_of(r);
         int lim = p.kv_hi - 1;
         if (p.causal_pos0 >= 0) lim = (int) min((int64_t) lim, p.causal_pos0 + tok);
-        if (p.row_lim) {
-            const int hq = kvh * p.G + (r - tok * p.G);
-            lim = min(lim, p.row_lim[((int64_t) (b % p.m_ne3) * p.m_ne2 + hq % p.m_ne2) * p.T + tok]);
-        }
+        if constexpr (has_mask) lim = min(lim, mtab[2 * unit_of(rr)]);
         return lim;
     };
     // this lane's row and limit; the wave's smallest limit over its valid
@@ -188,9 +262,6 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     auto kbuf = [&](const int t) { return kring + (t % NK) * kTileBytes; };
     auto vbuf = [&](const int t) { return vring + (t % NV) * kTileBytes; };
     const uint32_t lds0 = lds_addr(lds);
-
-    // gated behind the mask pass: the split-KV kernel takes a rejected mask
-    if (p.gate && __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) return;
 
     // ---- producer waves ----
     if (producer) {
@@ -266,7 +337,22 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     const float tau = kTau * kLog2e / cexp;               // kTau in units of s
     floatx16 o[4];
     float m_run = -AL_INF, l_run = 0.0f;
-    if (!producer) {
+    // The computing waves' work, compiled twice: GEN = the general-mask
+    // mode, so that its per-value mask reads cost the fast loop nothing.
+    auto compute = [&](auto gen_tag) {
+        constexpr bool GEN = decltype(gen_tag)::value;
+        // general mode: this lane's mask row and the factor of its values
+        // (ALiBi slope, arm.cpp:2294, over the scale the scores lack)
+        const _Float16 * mrow = nullptr;
+        float mslope = 0.0f;
+        if constexpr (GEN) {
+            mrow = (const _Float16 *) mask_row(rvalid ? rr : 0);
+            const uint32_t hq = (uint32_t) (kvh * p.G + (row0 + rr) - tok_of(row0 + rr) * p.G);
+            const float slope = p.max_bias > 0.0f ? (hq < p.n_head_log2 ? powf(p.m0, (float) (hq + 1))
+                                                                         : powf(p.m1, (float) (2 * (hq - p.n_head_log2) + 1)))
+                                                  : 1.0f;
+            mslope = SOFTCAP ? slope : slope / p.scale;
+        }
         // Q^T B operands: row rr (token r / G, head kvh G + r % G), dims
         // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers
         half8 qf[8];
@@ -331,7 +417,26 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
 #pragma unroll
                     for (int v = 0; v < 16; ++v) sc[cb][v] = p.softcap * tanhf(sc[cb][v] * p.scale);
             }
-            if (c0 + kTC - 1 > lim_min) {
+            if constexpr (GEN) {
+                // s + slope * mask in the units the scores are kept in (raw
+                // dot products: the mask term divided by the scale); cells
+                // past the row's extent -inf (arm.cpp:2310-2343)
+                // four cells at a time, each group's loads kept in its slot
+                // (a cold path: few registers rather than latency hiding)
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int w4 = 0; w4 < 4; ++w4) {
+                        const int cg = c0 + 32 * cb + 8 * w4 + 4 * h;
+                        float mv[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) mv[e] = cg + e <= lim ? (float) mrow[cg + e] : 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            sc[cb][4 * w4 + e] = cg + e <= lim ? sc[cb][4 * w4 + e] + mslope * mv[e] : -AL_INF;
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+            } else if (c0 + kTC - 1 > lim_min) {
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
@@ -372,7 +477,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         //    (four slots of four MFMAs, V operands read one slot ahead).
         // P^T operand kk holds cells 16 kk .. 16 kk + 15, i.e. registers
         // 8 (kk & 1) .. + 7 of S^T block kk / 2.
-        float mx;                                 // lane max of S(i + 1), from body(i)
+        float mx;                                 // lane max of S(i + 1), from body(i) (fast mode)
         auto body = [&](const int i, const bool qk, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
             const float mc = m_run == -AL_INF ? 0.0f : m_run * cexp;
             // the buffers' offsets as opaque values: otherwise the compiler
@@ -418,9 +523,11 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (qk) prepare(nxt, tile_c0(i + 1));
-            // the lane max of S(i + 1) in the slots of phase B (from slot 1
-            // on, when the last QK^T results are ready)
+            // fast mode: S(i + 1) prepared here and its lane max taken in the
+            // slots of phase B (from slot 1 on, when the last QK^T results
+            // are ready); general mode prepares it after the body
+            constexpr bool fold = !GEN;
+            if (fold && qk) prepare(nxt, tile_c0(i + 1));
             float mx0 = -AL_INF, mx1 = -AL_INF;
             const half2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
 #pragma unroll
@@ -429,7 +536,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
 #pragma unroll
                     for (int db = 0; db < 4; ++db) vn[db] = v_read(vb_, kk + 1, db);
                 }
-                if (qk && kk > 0 && kk < 3) {             // slot 1: block 0, slot 2: block 1
+                if (fold && qk && kk > 0 && kk < 3) {     // slot 1: block 0, slot 2: block 1
                     const floatx16 & x = nxt[kk - 1];
                     float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
 #pragma unroll
@@ -474,7 +581,8 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             auto iteration = [&](const int i, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
                 __syncthreads();                  // (B_i) K(i + 1), V(i) landed; iteration i - 1 done
                 body(i, true, cur, nxt);
-                if (__any(mx > m_run + tau)) rescale(nxt);
+                if constexpr (GEN) finish_scores(nxt, tile_c0(i + 1));
+                else if (__any(mx > m_run + tau)) rescale(nxt);
             };
             int i = 0;
             for (; i + 2 < NI; i += 2) {
@@ -490,6 +598,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             else body(i, false, s0, s1);
         }
         __syncthreads();                          // (3) rings free
+    };
+    if (!producer) {
+        if (MASK && general) compute(std::bool_constant<MASK>{});
+        else compute(std::false_type{});
     }
     float m_nat = m_run == -AL_INF ? -AL_INF : m_run * (cexp / kLog2e);
     float l_row = pair_sum(l_run);
@@ -614,78 +726,28 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     }
 }
 
-// One wavefront per mask row (token t of mask slice (i2, i3)), four rows
-// per workgroup, over cells [0, n_kv): the last cell holding +-0 (-1 if
-// none) into lims, and 1 into gate[0] when the row is not a run of zeros
-// followed by -inf (another value, or a zero after a -inf). Rows are read
-// 16 bytes (8 cells) per lane and load; the plan requires 16-byte aligned
-// mask rows.
-__global__ __launch_bounds__(256) void mask_limits_kernel(const FattnParams p, int32_t * lims, int * gate) {
-    const int lane = threadIdx.x & 63;
-    const int t = 4 * blockIdx.x + (threadIdx.x >> 6), i2 = blockIdx.y, i3 = blockIdx.z;
-    if (t >= p.T) return;
-    const char * rowp = p.mask + (int64_t) t * p.m_nb1 + (int64_t) i2 * p.m_nb2 + (int64_t) i3 * p.m_nb3;
-    int last0 = -1, first_inf = INT32_MAX, bad = 0;
-    auto classify = [&](const uint32_t hb, const int c) {
-        if ((hb & 0x7fffu) == 0) last0 = max(last0, c);
-        else if (hb == 0xfc00u) first_inf = min(first_inf, c);
-        else bad = 1;
-    };
-    // eight 16-byte loads per lane in flight at once (4096 cells per round)
-    const int n8 = p.n_kv >> 3;
-    for (int j0 = 0; j0 < n8; j0 += 8 * 64) {
-        uint4 w[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = j0 + 64 * u + lane;
-            w[u] = j < n8 ? *(const uint4 *) (rowp + 16 * (int64_t) j) : uint4{0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u};
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int j = j0 + 64 * u + lane;
-            if (j >= n8) continue;
-            const uint32_t x[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                classify(x[e] & 0xffffu, 8 * j + 2 * e);
-                classify(x[e] >> 16, 8 * j + 2 * e + 1);
-            }
-        }
-    }
-    for (int c = 8 * n8 + lane; c < p.n_kv; c += 64) classify(((const uint16_t *) rowp)[c], c);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        last0 = max(last0, __shfl_xor(last0, off));
-        first_inf = min(first_inf, __shfl_xor(first_inf, off));
-        bad |= __shfl_xor(bad, off);
-    }
-    if (lane == 0) {
-        lims[((int64_t) i3 * p.m_ne2 + i2) * p.T + t] = last0;
-        if (bad || last0 > first_inf) __hip_atomic_store(gate, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
 }  // namespace
 
-hipError_t fattn_mask_limits_launch(const FattnParams & p, int32_t * lims, int * gate, hipStream_t stream) {
-    const dim3 grid((unsigned) ((p.T + 3) / 4), (unsigned) p.m_ne2, (unsigned) p.m_ne3);
-    hipLaunchKernelGGL(mask_limits_kernel, grid, dim3(256), 0, stream, p, lims, gate);
-    return hipGetLastError();
-}
-
 size_t fattn_prefill_lds_bytes() { return (size_t) kLds; }
+
+template <int RG>
+static void launch_rg(const FattnParams & p, const dim3 grid, hipStream_t stream) {
+    const dim3 block(2 * kWaves * 64);
+    const bool sc = p.softcap != 0.0f, mk = p.mask != nullptr;
+    if (sc) {
+        if (mk) hipLaunchKernelGGL((fattn_prefill_kernel<RG, true, true>), grid, block, 0, stream, p);
+        else    hipLaunchKernelGGL((fattn_prefill_kernel<RG, true, false>), grid, block, 0, stream, p);
+    } else {
+        if (mk) hipLaunchKernelGGL((fattn_prefill_kernel<RG, false, true>), grid, block, 0, stream, p);
+        else    hipLaunchKernelGGL((fattn_prefill_kernel<RG, false, false>), grid, block, 0, stream, p);
+    }
+}
 
 hipError_t fattn_prefill_launch(const FattnParams & p, int rows_per_tile, hipStream_t stream) {
     if (p.n_split < 1 || p.n_split > kMaxPrefillSplit || (rows_per_tile != 64 && rows_per_tile != 128))
         return hipErrorInvalidValue;
     const dim3 grid((unsigned) p.Hkv, (unsigned) p.n_split, (unsigned) ((int64_t) p.n_row_tiles * p.B));
-    const bool sc = p.softcap != 0.0f;
-    if (rows_per_tile == 128) {
-        if (sc) hipLaunchKernelGGL((fattn_prefill_kernel<4, true>), grid, dim3(2 * kWaves * 64), 0, stream, p);
-        else    hipLaunchKernelGGL((fattn_prefill_kernel<4, false>), grid, dim3(2 * kWaves * 64), 0, stream, p);
-    } else {
-        if (sc) hipLaunchKernelGGL((fattn_prefill_kernel<2, true>), grid, dim3(2 * kWaves * 64), 0, stream, p);
-        else    hipLaunchKernelGGL((fattn_prefill_kernel<2, false>), grid, dim3(2 * kWaves * 64), 0, stream, p);
-    }
+    if (rows_per_tile == 128) launch_rg<4>(p, grid, stream);
+    else launch_rg<2>(p, grid, stream);
     return hipGetLastError();
 }

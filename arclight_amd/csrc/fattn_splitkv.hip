@@ -45,30 +45,6 @@ __global__ __launch_bounds__(W * 64) void fattn_splitkv_kernel(const FattnParams
     __shared__ float lds[NSLOT * ROWS * kRowStride];
     __shared__ int s_last;
 
-    // Gated behind the prefill kernel: only when the mask pass rejected the
-    // mask. Each workgroup reads the gate (the mask pass that wrote it ended
-    // before this kernel began, so a relaxed load sees it); an open gate
-    // (accepted mask) ends the workgroup at once, untouched. A set gate stays
-    // set until every workgroup has read it (the arrival below depends on
-    // the loaded value) and arrived; the last to arrive clears the gate and
-    // the arrival count for the next call in stream order.
-    if (p.gate) {
-        if (threadIdx.x == 0) {
-            const int gv = __hip_atomic_load(p.gate, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (gv != 0) {
-                unsigned * arrived = (unsigned *) (p.gate + 1);
-                if (add_agent(arrived, 1u) == gridDim.x - 1) {
-                    st_agent_u32(arrived, 0u);
-                    __hip_atomic_store(p.gate, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            s_last = gv;
-        }
-        __syncthreads();
-        if (s_last == 0) return;
-        __syncthreads();                                          // s_last is reused below
-    }
-
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4;

@@ -234,7 +234,7 @@ def bench_other_configs(lib, stream, a):
     for name, kw in [("prefill 2048 tokens in 8 causal ubatches of 256 (ArcLight's default ubatch), Qwen3-4B shape, "
                       "36 layers", dict(chunk=256)),
                      ("prefill 2048 tokens in 4 causal chunks of 512, explicit f16 mask and no length hints (the "
-                      "call as nnml makes it: mask pass, then the prefill kernel), Qwen3-4B shape, 36 layers",
+                      "call as nnml makes it: the prefill kernel reads the mask), Qwen3-4B shape, 36 layers",
                       dict(chunk=512, explicit_mask=True))]:
         r = bench_prefill(lib, stream, a, **kw)
         out.append({"workload": name, "value": round(r["tflops"], 2), "unit": "TFLOP/s",

@@ -94,14 +94,9 @@ typedef struct al_tensor {
  * its own buffer for the current device and args->stream (allocated on first
  * use, grown when needed; a graph captured on a stream uses that stream's).
  * A caller workspace must be zero-filled before its first use. Its first
- * 256 KiB hold arrival counters; the last two words of that region gate a
- * many-row call that carries a mask tensor. Every call leaves the region at
- * zero again. Per-call merge records follow it, then (for a many-row call
- * with a mask tensor) the row limits that a pass over the mask writes: the
- * last visible cell of each mask row, which the prefill kernel reads when
- * every row is a run of zeros followed by -inf; otherwise the gate sends
- * the call to the general kernel. Calls that share one workspace must be
- * ordered on one stream.
+ * 256 KiB hold arrival counters, which every call leaves at zero again;
+ * per-call merge records follow them. Calls that share one workspace must
+ * be ordered on one stream.
  *
  * dyn_len: for a call captured once into a HIP graph and replayed for every
  * decode step (the GPU form of the reference's graph reuse while n_kv stays
@@ -164,8 +159,8 @@ uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * validation, kernels and results as al_fattn_f16; args->workspace is
- * ignored. The scratch (arrival counters and gate, split-KV merge records,
- * row limits) is a file-scope device array of
+ * ignored. The scratch (arrival counters and merge records) is a file-scope
+ * device array of
  * AL_FATTN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. A
  * call that needs more (al_fattn_workspace_bytes) fails with
  * AL_ERR_WORKSPACE. Every call on one GPU shares that array: calls that

@@ -259,6 +259,29 @@ def test_prefill_kernel_gqa8_noncausal_sinks_softcap(gpu):
            kv_len=1000, causal_pos0=744)
 
 
+def test_prefill_kernel_explicit_masks(gpu):
+    # The prefill kernel reads an explicit mask itself: prefix masks (runs
+    # of zeros then -inf) as per-row extents, any other mask value by value
+    # in the tiles of its rows (general mode), with ALiBi, softcap, sinks,
+    # per-head mask slices and two streams.
+    rng = np.random.default_rng(21)
+    T, n_kv = 512, 1536
+    q, k, v = O.make_inputs(2101, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+    m = O.causal_mask(T, n_kv, 1024, kv_len=1500)
+    _check("prefill, causal prefix mask", q, k, v, m, scale=SCALE)
+    mb = m.copy()
+    mb[0, 0, :T, :1024] = np.where(mb[0, 0, :T, :1024] == 0, rng.uniform(-3, 0, (T, 1024)), -np.inf).astype(np.float16)
+    mb[0, 0, 5:40, 100:300] = -np.inf                                 # holes inside some rows
+    _check("prefill, general mask with biases and holes, ALiBi", q, k, v, mb, scale=SCALE, max_bias=8.0)
+    sinks = rng.standard_normal(32).astype(np.float32)
+    _check("prefill, general mask, softcap + sinks", q, k, v, mb, sinks, scale=SCALE * 4, logit_softcap=5.0)
+    # one mask slice per head (mask dim 2 = Hq) and two streams (dim 3 = 2)
+    q2, k2, v2 = O.make_inputs(2102, B=2, T=256, Hq=16, Hkv=4, n_kv=1024)
+    mh = np.broadcast_to(O.causal_mask(256, 1024, 700, kv_len=956), (2, 16, 256, 1024)).copy()
+    mh[1, 3, :, 200:220] = np.float16(-2.0)
+    _check("prefill, per-head general mask, 2 streams", q2, k2, v2, mh, scale=SCALE, max_bias=4.0)
+
+
 def test_prefill_kernel_streams_ragged(gpu):
     # two streams, rows not a multiple of 64, cells not a multiple of 32
     q, k, v = O.make_inputs(601, B=2, T=510, Hq=16, Hkv=4, n_kv=1111)

@@ -93,9 +93,9 @@ def test_prefill_chunks_equal_one_causal_call(gpu):
 
 def test_prefill_explicit_mask_on_the_prefill_kernel(gpu):
     # a 512-token causal chunk with the f16 mask tensor and no length hints:
-    # a mask of zero runs then -inf goes to the prefill kernel on the mask's
-    # row limits; a mask with a hole and biases goes to the split-KV kernel;
-    # and a plain mask again after that (each call clears the gate it used)
+    # a mask of zero runs then -inf becomes per-row extents in the prefill
+    # kernel; a mask with a hole and biases is taken value by value; and a
+    # plain mask again after that
     n_kv = 2048
     q, k, v = O.make_inputs(4096, T=512, Hq=32, Hkv=8, n_kv=n_kv)
     m = O.causal_mask(512, n_kv, 1536, kv_len=2000)

@@ -1,15 +1,15 @@
-"""Workspace and gate state across calls.
+"""Workspace state across calls, masked many-row calls in between.
 
-- A many-row call with a mask tensor whose split-KV fallback plans a single
-  split (Qwen3-32B shape, 1024-token chunk: 128 row tiles x 8 kv heads fill
-  the device) still keeps its row limits out of the arrival-counter region:
-  a multi-split decode call that follows on the same library workspace
-  matches the oracle.
-- Masked many-row calls on two streams, one mask accepted by the mask pass
-  and one rejected, overlap without touching each other's gate or records.
-- A captured masked call replayed first with a rejected mask and then with
-  an accepted one gives the oracle's result on every replay (the gate is
-  cleared within each call).
+- A many-row call with a mask tensor whose prefill plan has a single split
+  (Qwen3-32B shape, 1024-token chunk: 128 row tiles x 8 kv heads fill the
+  device) needs no workspace; a multi-split decode call that follows on the
+  library workspace matches the oracle, before and after masks the prefill
+  kernel takes value by value (a hole, biases).
+- Masked many-row calls on two streams, one mask a causal prefix and one
+  not, overlap without touching each other's records.
+- A captured masked call replayed first with a non-prefix mask and then with
+  a prefix one gives the oracle's result on every replay (nothing a call
+  decides about its mask outlives the call).
 
 Bar: max-abs <= 2e-3 and rel-L2 <= 1e-3 on the fp32 output against oracle
 O2, as everywhere.
@@ -55,25 +55,25 @@ def test_masked_single_split_prefill_then_decode(gpu):
     n_kv = pos0 + T
     q, k, v = O.make_inputs(77, T=T, Hq=64, Hkv=8, n_kv=n_kv)
     m = O.causal_mask(T, n_kv, pos0, kv_len=n_kv)
-    # the masked plan reserves the counter region (the gate lives there)
+    # one workgroup per row tile: no merge records, no counters
     need = fattn.workspace_bytes(fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v), fattn.upload_mask(m),
                                  None, _dst(q), scale=SCALE)
-    assert need >= 256 * 1024, need
+    assert need == 0, need
     rng = np.random.default_rng(5)
     sel = np.unique(np.concatenate([[0, 63, 64, T - 1], rng.choice(T, 20, replace=False)]))
-    _case("Qwen3-32B chunk 1024, explicit causal mask (accepted, single-split fallback plan)")
+    _case("Qwen3-32B chunk 1024, explicit causal mask (a prefix in every row)")
     got = run_gpu(q, k, v, m, scale=SCALE)
     assert_parity(got[:, sel], _sampled(q, k, v, m, sel), what="32B masked chunk")
     _case("decode after it on the library workspace")
     _decode_check(11)
     m2 = m.copy()
-    m2[..., 300] = -np.inf                           # a hole: the mask pass rejects it
-    _case("Qwen3-32B chunk 1024, mask with a hole (rejected)")
+    m2[..., 300] = -np.inf                           # a hole: taken value by value
+    _case("Qwen3-32B chunk 1024, mask with a hole")
     got = run_gpu(q, k, v, m2, scale=SCALE)
     assert_parity(got[:, sel], _sampled(q, k, v, m2, sel), what="32B masked chunk with hole")
-    _case("decode after the rejected mask")
+    _case("decode after the mask with a hole")
     _decode_check(12)
-    _case("accepted mask again")
+    _case("prefix mask again")
     got = run_gpu(q, k, v, m, scale=SCALE)
     assert_parity(got[:, sel], _sampled(q, k, v, m, sel), what="32B masked chunk again")
 
@@ -98,22 +98,22 @@ def test_masked_calls_on_two_streams(gpu):
         fattn.flash_attn_ext(dq, dk, dv, dm_bad, scale=SCALE, dst=outs_a[0], stream=sa)
         fattn.flash_attn_ext(dq, dk, dv, dm_ok, scale=SCALE, dst=outs_b[0], stream=sb)
         device.synchronize()
-        _case("two streams, rejected and accepted masks interleaved")
+        _case("two streams, non-prefix and prefix masks interleaved")
         for i in range(3):
             fattn.flash_attn_ext(dq, dk, dv, dm_bad, scale=SCALE, dst=outs_a[i], stream=sa)
             fattn.flash_attn_ext(dq, dk, dv, dm_ok, scale=SCALE, dst=outs_b[i], stream=sb)
         device.synchronize()
         fattn.device_errors()
         for i in range(3):
-            assert_parity(outs_a[i].numpy(np.float32), ref_bad, what=f"stream A (rejected mask) call {i}")
-            assert_parity(outs_b[i].numpy(np.float32), ref_ok, what=f"stream B (accepted mask) call {i}")
+            assert_parity(outs_a[i].numpy(np.float32), ref_bad, what=f"stream A (non-prefix mask) call {i}")
+            assert_parity(outs_b[i].numpy(np.float32), ref_ok, what=f"stream B (prefix mask) call {i}")
     finally:
         device.synchronize()
         sa.destroy()
         sb.destroy()
 
 
-def test_masked_call_replayed_with_rejected_then_accepted_mask(gpu):
+def test_masked_call_replayed_with_nonprefix_then_prefix_mask(gpu):
     from arclight_amd import device, fattn
     n_kv = 1024
     q, k, v = O.make_inputs(99, T=512, Hq=32, Hkv=8, n_kv=n_kv)

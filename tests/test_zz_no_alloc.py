@@ -3,9 +3,9 @@ al_fattn_f16 on the same inputs, through the C ABI: two calls in a row, the
 second with a smaller input, each bit-identical to the allocating entry
 point's result (same plan and kernels) and within the parity bar of oracle
 O2 (max-abs <= 2e-3, rel-L2 <= 1e-3). Covers a multi-split decode (counters
-and merge records in the device array), a masked many-row call (gate and
-row limits there too), and a call that needs more scratch than the array
-holds (rejected with AL_ERR_WORKSPACE)."""
+and merge records in the device array), masked many-row calls (one whose
+mask is a causal prefix, one taken value by value), and a call that needs
+more scratch than the array holds (rejected with AL_ERR_WORKSPACE)."""
 import ctypes
 import math
 
@@ -57,7 +57,7 @@ def test_noalloc_matches_allocating_entry(gpu):
     _check("decode 16384 cells", q, k, v, kv_len=16384)
     q, k, v = O.make_inputs(502, T=1, Hq=32, Hkv=8, n_kv=4096)
     _check("decode 4000 of 4096 cells (smaller)", q, k, v, kv_len=4000)
-    # masked many-row calls: an accepted mask, then a smaller rejected one
+    # masked many-row calls: a causal prefix mask, then a smaller one with a hole
     q, k, v = O.make_inputs(503, T=512, Hq=32, Hkv=8, n_kv=2048)
     _check("512-token chunk, explicit causal mask", q, k, v, O.causal_mask(512, 2048, 1536, kv_len=2000))
     q, k, v = O.make_inputs(504, T=128, Hq=32, Hkv=8, n_kv=1024)
@@ -69,13 +69,14 @@ def test_noalloc_matches_allocating_entry(gpu):
 def test_noalloc_rejects_oversized_call(gpu):
     from arclight_amd import _lib, abi, device, fattn
     lib = _lib.load()
-    # a masked 1008-token call: its general-kernel plan has 63 row tiles x 8
-    # kv heads in 2 splits, 504 x 2 records of 64 rows x 528 bytes (34 MB)
+    # a masked 1008-token call whose mask rows are not 16-byte aligned (1025
+    # columns), so the split-KV kernel takes it: 63 row tiles x 8 kv heads
+    # in 2 splits, 504 x 2 records of 64 rows x 528 bytes (34 MB)
     T, n_kv = 1008, 1024
     dq = device.DeviceTensor.empty((1, T, 32, 128), np.float32, axes=abi.Q_AXES)
     dk = device.DeviceTensor.empty((1, n_kv, 8, 128), np.uint16, axes=abi.KV_AXES)
     dv = device.DeviceTensor.empty((1, n_kv, 8, 128), np.uint16, axes=abi.KV_AXES)
-    dm = fattn.upload_mask(O.causal_mask(T, n_kv, 16, kv_len=n_kv))
+    dm = fattn.upload_mask(O.causal_mask(T, n_kv + 1, 16, kv_len=n_kv))
     dst = device.DeviceTensor.empty((1, T, 32, 128), np.float32, axes=abi.DST_AXES)
     a = fattn.fattn_args(dq, dk, dv, dm, None, dst, scale=SCALE)
     need = lib.al_fattn_workspace_bytes(ctypes.byref(a))
