@@ -173,6 +173,11 @@ struct Plan {
 
 bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
 
+// ceil(2^32 / d) for d >= 2, 0 for d <= 1: x / d = umulhi(x, magic) when x d < 2^32
+uint32_t magic_u32(const int64_t d) {
+    return d > 1 ? (uint32_t) (((1ull << 32) + (uint64_t) d - 1) / (uint64_t) d) : 0u;
+}
+
 // AL_FATTN_PREFILL=0 keeps many-row calls on the split-KV kernel.
 bool prefer_prefill() {
     static bool v = [] {
@@ -329,7 +334,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     p.dst = (char *) d.data; p.dst_nb1 = d.nb[1];
     p.T = (int32_t) T; p.Hq = (int32_t) Hq; p.Hkv = (int32_t) Hkv; p.G = (int32_t) (Hq / Hkv); p.B = (int32_t) B;
     p.R = p.T * p.G;
-    p.g_magic = p.G > 1 ? (uint32_t) (((1ull << 32) + (uint64_t) p.G - 1) / (uint64_t) p.G) : 0u;
+    p.g_magic = magic_u32(p.G);
     p.rk3 = (int32_t) (B / k.ne[3]); p.rv3 = (int32_t) (B / v.ne[3]);
     p.n_kv = (int32_t) n_kv;
     p.kv_hi = (int32_t) ((a->kv_len <= 0 || a->kv_len > n_kv) ? n_kv : a->kv_len);
@@ -382,6 +387,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.n_row_tiles = (int32_t) prefill_tiles;
         p.n_split = (int32_t) prefill_split;
         p.cells_per_split = 0;
+        p.split_magic = magic_u32(prefill_split * in_wg_split);
+        p.tiles_magic = magic_u32(prefill_tiles);
         if (prefill_split > 1) {
             pl.counters_bytes = kFattnCounterBytes;
             pl.part_bytes = prefill_part;

@@ -62,6 +62,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
     __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
+    prefetch_params(p);
     int & s_last = *(int *) qlds;                         // after the prologue the query rows are dead
 
     const int lane = threadIdx.x & 63;

@@ -19,6 +19,8 @@ struct FattnParams {
 
     int32_t T, Hq, Hkv, G, B, R;    // R = T*G query rows per kv head
     uint32_t g_magic;               // ceil(2^32 / G) (0 for G = 1): r / G = umulhi(r, g_magic) for r G < 2^32
+    uint32_t split_magic;           // prefill: ceil(2^32 / (n_split * in-workgroup splits)) (0 for 1)
+    uint32_t tiles_magic;           // prefill: ceil(2^32 / n_row_tiles) (0 for 1)
     int32_t rk3, rv3;               // q streams per k / v stream
     int32_t n_kv;                   // cells addressable in k/v
     int32_t kv_hi;                  // cells >= kv_hi are masked for all rows

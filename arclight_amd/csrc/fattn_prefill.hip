@@ -105,6 +105,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     using S = Shape<RG>;
     constexpr int ROWS = S::ROWS, NK = S::NK, NV = S::NV, PER = S::PER;
     __shared__ __attribute__((aligned(1024))) char lds[kLds];
+    prefetch_params(p);
 
     // Waves 0..3 compute (one per SIMD); waves 4..7 (one per SIMD too) only
     // move K/V tiles and query rows into LDS: an LDS-DMA instruction stalls
@@ -212,32 +213,40 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
 
     // Last visible cell of a row: the length / causal rule, narrowed by the
     // explicit mask's extent when a mask tensor came with the call.
-    auto row_lim = [&](const int rr) {                    // rr: row within the tile, < rows_here
-        const int r = row0 + rr;
-        const int tok = tok_of(r);
-        int lim = p.kv_hi - 1;
-        if (p.causal_pos0 >= 0) lim = (int) min((int64_t) lim, p.causal_pos0 + tok);
-        if constexpr (has_mask) lim = min(lim, mtab[2 * unit_of(rr)]);
-        return lim;
+    auto rule_lim = [&](const int tok) {                  // the length / causal rule for token tok
+        int l = p.kv_hi - 1;
+        if (p.causal_pos0 >= 0) l = (int) min((int64_t) l, p.causal_pos0 + tok);
+        return l;
     };
     // this lane's row and limit; the wave's smallest limit over its valid
     // rows (a tile within it is visible to every row of the wave); hi_wg,
-    // one past the last cell any row of the workgroup sees (every wave
-    // evaluates all rows: no LDS before the rings fill)
+    // one past the last cell any row of the workgroup sees
     const int rr = 32 * rg + lr;
     const bool rvalid = rr < rows_here;
-    const int lim = rvalid ? row_lim(rr) : INT32_MAX;
-    int lim_min = lim, lim_max = -1;
+    int lim, lim_min, hi_wg;
+    if constexpr (has_mask) {
+        // every wave evaluates all rows of the tile, then reduces
+        auto row_lim = [&](const int r_) { return min(rule_lim(tok_of(row0 + r_)), mtab[2 * unit_of(r_)]); };
+        lim = rvalid ? row_lim(rr) : INT32_MAX;
+        int lmin = lim, lmax = -1;
 #pragma unroll
-    for (int q = 0; q < RG; ++q)
-        if (32 * q + lr < rows_here) lim_max = max(lim_max, q == rg ? lim : row_lim(32 * q + lr));
+        for (int q = 0; q < RG; ++q)
+            if (32 * q + lr < rows_here) lmax = max(lmax, q == rg ? lim : row_lim(32 * q + lr));
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        lim_min = min(lim_min, __shfl_xor(lim_min, off));
-        lim_max = max(lim_max, __shfl_xor(lim_max, off));
+        for (int off = 32; off >= 1; off >>= 1) {
+            lmin = min(lmin, __shfl_xor(lmin, off));
+            lmax = max(lmax, __shfl_xor(lmax, off));
+        }
+        lim_min = __builtin_amdgcn_readfirstlane(lmin);
+        hi_wg = __builtin_amdgcn_readfirstlane(lmax) + 1;
+    } else {
+        // the rule does not decrease from row to row: the wave's first row
+        // has its smallest limit, the tile's last row the largest (scalar
+        // arithmetic, no cross-lane reductions on the way to the first loads)
+        lim = rvalid ? rule_lim(tok_of(row0 + rr)) : INT32_MAX;
+        lim_min = 32 * rg < rows_here ? rule_lim(tok_of(row0 + 32 * rg)) : INT32_MAX;
+        hi_wg = rule_lim(tok_of(row0 + rows_here - 1)) + 1;
     }
-    lim_min = __builtin_amdgcn_readfirstlane(lim_min);
-    const int hi_wg = __builtin_amdgcn_readfirstlane(lim_max) + 1;
 
     // Tiles of the whole row tile: NT of 64 cells; split s_all of n_all
     // takes tiles j n_all + s_all, visited from j = rot on. All splits run
@@ -247,8 +256,13 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     const int n_all = p.n_split * S::SP;
     const int s_all = sx * S::SP + si;
     const int NT = (max(hi_wg, 0) + kTC - 1) / kTC;
-    const int NI = __builtin_amdgcn_readfirstlane((NT + n_all - 1) / n_all);
-    const int rot = __builtin_amdgcn_readfirstlane(NI > 0 ? (rt * NI) / p.n_row_tiles : 0);
+    // NI = ceil(NT / n_all) and rot ~ rt NI / n_row_tiles by multiply-high
+    // with the plan's reciprocals (0: divisor 1); rot only staggers the
+    // splits' first tiles, so its rounding only needs rot < NI
+    const int NI = __builtin_amdgcn_readfirstlane(
+        p.split_magic ? (int) __umulhi((uint32_t) (NT + n_all - 1), p.split_magic) : NT);
+    const int rot = __builtin_amdgcn_readfirstlane(
+        NI > 0 ? min((int) __umulhi((uint32_t) (rt * NI), p.tiles_magic), NI - 1) : 0);
     const int n_vis = max(min(hi_wg, p.n_kv), 1);
     auto tile_c0 = [&](const int i) {                     // branch-free: selects only
         int j = i + rot;

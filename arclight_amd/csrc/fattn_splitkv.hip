@@ -44,6 +44,7 @@ __global__ __launch_bounds__(W * 64) void fattn_splitkv_kernel(const FattnParams
     constexpr int NSLOT = ((W / 2) * ROWS * kRowStride * 4 <= 40960) ? W / 2 : 1;
     __shared__ float lds[NSLOT * ROWS * kRowStride];
     __shared__ int s_last;
+    prefetch_params(p);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;

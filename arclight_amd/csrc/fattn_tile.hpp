@@ -5,6 +5,7 @@
 
 #include "device_common.hpp"
 #include "fattn_kernels.hpp"
+#include "kernel_args.hpp"
 
 namespace fattn {
 
@@ -14,6 +15,7 @@ constexpr int kMaxSplit = kFattnMaxSplit;
 constexpr float kTau = 8.0f;                      // lazy-rescale threshold (natural log units)
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
 
 // Raw buffer over [base, base + bytes): 32-bit offsets, loads past the end
 // return zeros.

@@ -13,6 +13,7 @@
 namespace {
 
 __global__ __launch_bounds__(256) void set_rows_kernel(const SetRowsParams p) {
+    prefetch_params(p);
     set_rows_row(p, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 

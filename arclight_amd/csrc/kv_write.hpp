@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/arclight_fattn.h"
+#include "kernel_args.hpp"
 
 struct SetRowsParams {
     const char * src;  int64_t s_nb1, s_nb2, s_nb3;   // f32 [nc, nr, ne2, ne3]

@@ -31,6 +31,7 @@
 #include <mutex>
 
 #include "../../include/arclight_matmul.h"
+#include "kernel_args.hpp"
 #include "runtime.hpp"
 
 namespace {
@@ -210,6 +211,7 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
                                                              const char * x, int64_t x_nb1, int T,
                                                              char * __restrict__ y, int64_t y_nb1) {
     extern __shared__ __align__(16) char lds[];
+    prefetch_params(w_nb1, y_nb1, blockDim.x);
     const int nb = K / 32;
     int8_t * qs = (int8_t *) lds;                                       // [T][K]
     float * dx = (float *) (lds + T * K);                               // [T][nb]

@@ -116,6 +116,7 @@ __device__ __forceinline__ void norm_rope_row(const NormRopeParams & p, const in
 
 template <int MODE, bool CACHE>
 __global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) {
+    prefetch_params(p);
     norm_rope_row<MODE, CACHE>(p, blockIdx.y * 4 + (threadIdx.x >> 6), blockIdx.x, threadIdx.x & 63);
 }
 
@@ -125,6 +126,7 @@ __global__ __launch_bounds__(256) void norm_rope_kernel(const NormRopeParams p) 
 template <int MODE>
 __global__ __launch_bounds__(256) void attn_inputs_kernel(const NormRopeParams q, const NormRopeParams k,
                                                           const SetRowsParams v, const int yq, const int yk) {
+    prefetch_params(q, k, v, yq, yk);
     const int by = blockIdx.y;
     const int hw = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (by < yq) norm_rope_row<MODE, false>(q, by * 4 + hw, blockIdx.x, lane);
