@@ -324,14 +324,23 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // have been for i = 1 - NK .. -1, interleaved the same way: RG = 2:
         // K0 V0 K1 V1; RG = 4: V0 K0 V1 K1 V2 K2 V3 K3 V4. Before B_i: K(i + 1)
         // and V(i) landed (2 NK - 3 tiles issued after K(i + 1) may still fly).
+        // The first tiles go out before the computing waves load the query
+        // rows (barrier Q): the whole device reads its query rows at once,
+        // and K0 queued behind them would hold up the first scores.
         if (NI > 0) {
             if constexpr (RG == 4) {
-                dma_v(0); dma_k(0); dma_v(1); dma_k(1); dma_v(2); dma_k(2); dma_v(3); dma_k(3); dma_v(4);
+                dma_v(0); dma_k(0);
+                __syncthreads();                  // (Q)
+                dma_v(1); dma_k(1); dma_v(2); dma_k(2); dma_v(3); dma_k(3); dma_v(4);
                 wait_vm<7 * PER>();               // V0, K0 landed
             } else {
-                dma_k(0); dma_v(0); dma_k(1); dma_v(1);
+                dma_k(0);
+                __syncthreads();                  // (Q)
+                dma_v(0); dma_k(1); dma_v(1);
                 wait_vm<3 * PER>();               // K0 landed
             }
+        } else {
+            __syncthreads();                      // (Q)
         }
         __syncthreads();                          // (1) K0 visible
         for (int i = 0; i < NI; ++i) {
@@ -370,6 +379,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // Q^T B operands: row rr (token r / G, head kvh G + r % G), dims
         // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers
         half8 qf[8];
+        __syncthreads();                          // (Q) the first K/V tiles are on their way
         {
             const int r = row0 + (rvalid ? rr : 0);
             const int tk = tok_of(r);
