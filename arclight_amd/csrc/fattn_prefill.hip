@@ -447,26 +447,33 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 // past the row's extent -inf (arm.cpp:2310-2343)
                 // four cells at a time, each group's loads kept in its slot
                 // (a cold path: few registers rather than latency hiding)
+                // (cell c0 + 4 h + off visible when off <= d; the offsets
+                // are immediates of the compares and loads)
+                const int d = lim - c0 - 4 * h;
+                const _Float16 * mt = mrow + c0 + 4 * h;
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                     for (int w4 = 0; w4 < 4; ++w4) {
-                        const int cg = c0 + 32 * cb + 8 * w4 + 4 * h;
+                        const int og = 32 * cb + 8 * w4;
                         float mv[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) mv[e] = cg + e <= lim ? (float) mrow[cg + e] : 0.0f;
+                        for (int e = 0; e < 4; ++e) mv[e] = og + e <= d ? (float) mt[og + e] : 0.0f;
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            sc[cb][4 * w4 + e] = cg + e <= lim ? sc[cb][4 * w4 + e] + mslope * mv[e] : -AL_INF;
+                            sc[cb][4 * w4 + e] = og + e <= d ? sc[cb][4 * w4 + e] + mslope * mv[e] : -AL_INF;
                         __builtin_amdgcn_sched_barrier(0);
                     }
             } else if (c0 + kTC - 1 > lim_min) {
+                // cell c0 + 4 h + off is visible when off <= d: one register
+                // per tile, the offsets are immediates
+                const int d = lim - c0 - 4 * h;
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
-                        const int c = c0 + 32 * cb + (v & 3) + 8 * (v >> 2) + 4 * h;
-                        sc[cb][v] = c <= lim ? sc[cb][v] : -AL_INF;
+                        const int off = 32 * cb + (v & 3) + 8 * (v >> 2);
+                        sc[cb][v] = off <= d ? sc[cb][v] : -AL_INF;
                     }
             }
         };
