@@ -76,6 +76,7 @@ SIGNATURES = {
     "al_rms_norm_rope_f32": (_I, [ctypes.POINTER(abi.AlTensor)] * 3 + [ctypes.c_float, ctypes.POINTER(abi.AlRopeParams)]
                              + [ctypes.POINTER(abi.AlTensor)] * 2 + [_VP]),
     "al_attn_inputs_f32": (_I, [ctypes.POINTER(abi.AlAttnInputsArgs), _VP]),
+    "al_fattn_f16_with_inputs": (_I, [ctypes.POINTER(abi.AlAttnInputsArgs), ctypes.POINTER(abi.AlFattnArgs)]),
     # include/arclight_matmul.h
     "al_mul_mat_q4_0_f32": (_I, [ctypes.POINTER(abi.AlTensor)] * 3 + [_VP]),
 }

@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/arclight_fattn.h"
+#include "../../include/arclight_prologue.h"
 #include "fattn_kernels.hpp"
 #include "kv_write.hpp"
 #include "runtime.hpp"
@@ -493,7 +494,11 @@ extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
 // One call with the plan's workspace: the caller's, else the library's for
 // the stream (library_workspace), or with noalloc_ws set the no-allocation
 // entry's device array, which is never grown.
-static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_bytes) {
+// fused: the attention inputs folded into the decode kernel (fmode: their
+// rotation); AL_ERR_UNSUPPORTED before any launch when the plan is not the
+// decode kernel in a shape that takes them.
+static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_bytes,
+                     const DecodeInputs * fused = nullptr, int fmode = 0) {
     int n_cu = 0, lds = 0;
     int rc = al_device_cu_count(&n_cu);
     if (rc == AL_OK) rc = al_device_lds_per_block(&lds);
@@ -501,6 +506,10 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
     Plan pl;
     rc = make_plan(a, n_cu, lds, &pl);
     if (rc != AL_OK) return rc;
+    if (fused && (pl.kernel != kDecode || !fattn_decode_fused_ok(pl.waves, pl.stages) || pl.p.R > 16 ||
+                  pl.p.B != 1 || pl.p.mask))
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn_with_inputs: the call does not run on the decode kernel "
+                       "(up to 16 rows per kv head, one stream, no mask tensor)");
     const size_t need = pl.counters_bytes + pl.part_bytes;
     if (need) {
         void * ws = noalloc_ws ? noalloc_ws : a->workspace;
@@ -524,7 +533,10 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
     hipError_t e;
     switch (pl.kernel) {
         case kPrefill: e = fattn_prefill_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
-        case kDecode:  e = fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream); break;
+        case kDecode:
+            e = fused ? fattn_decode_launch_fused(pl.p, *fused, fmode, pl.waves, pl.stages, (hipStream_t) a->stream)
+                      : fattn_decode_launch(pl.p, pl.waves, pl.stages, (hipStream_t) a->stream);
+            break;
         default:       e = fattn_splitkv_launch(pl.p, pl.rows_per_tile, (hipStream_t) a->stream); break;
     }
     if (e != hipSuccess) return al_hip_fail(e, "fattn: kernel launch");
@@ -532,6 +544,32 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
 }
 
 extern "C" int al_fattn_f16(const al_fattn_args * a) { return fattn_run(a, nullptr, 0); }
+
+extern "C" int al_fattn_f16_with_inputs(const al_attn_inputs_args * in, const al_fattn_args * a) {
+    if (!in || !a) return al_fail(AL_ERR_INVALID, "fattn_with_inputs: null arguments");
+    DecodeInputs di;
+    int mode = 0;
+    int rc = attn_inputs_decode(in, &di, &mode);
+    if (rc != AL_OK) return rc;
+    // the attention's query operand is q_out (al_fattn q axes [D, T, Hq, B]),
+    // read here from the inputs' raw rows, which the kernel normalizes
+    const al_tensor & q = a->q, & qo = in->q_out;
+    if (q.data != qo.data || q.ne[0] != 128 || q.ne[1] != qo.ne[2] || q.ne[2] != qo.ne[1] || q.ne[3] != 1 ||
+        q.nb[1] != qo.nb[2] || q.nb[2] != qo.nb[1])
+        return al_fail(AL_ERR_INVALID, "fattn_with_inputs: the attention's q must view the inputs' q_out");
+    // the new tokens' cache rows are the attention's cells: the K / V views
+    // start at the caches with their row strides and 128-half heads
+    const al_tensor & k = a->k, & v = a->v;
+    if (k.data != in->k_cache.data || k.nb[1] != in->k_cache.nb[1] || k.nb[2] != 256 || k.ne[2] * 128 != in->k_cache.ne[0] ||
+        v.data != in->v_cache.data || v.nb[1] != in->v_cache.nb[1] || v.nb[2] != 256 || v.ne[2] * 128 != in->v_cache.ne[0])
+        return al_fail(AL_ERR_UNSUPPORTED, "fattn_with_inputs: the K / V views are not the caches the inputs write");
+    al_fattn_args aa = *a;
+    aa.q.data = in->q.data;
+    aa.q.nb[1] = in->q.nb[2];
+    aa.q.nb[2] = in->q.nb[1];
+    aa.q.nb[3] = in->q.nb[3];
+    return fattn_run(&aa, nullptr, 0, &di, mode);
+}
 
 extern "C" int al_fattn_f16_worker(const al_fattn_args * a, int ith, int nth) {
     if (nth < 1 || ith < 0 || ith >= nth) return al_fail(AL_ERR_INVALID, "fattn: worker %d of %d", ith, nth);

@@ -51,9 +51,13 @@ namespace {
 using namespace fattn;
 
 constexpr int kSC = 16;                                   // cells per stage
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
-template <int WS, int NB, bool HAS_MASK, int RB>
-__global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p) {
+// FM < 0: the query rows come ready in p.q; FM >= 0: the attention inputs
+// folded in (DecodeInputs), FM the rotation mode.
+template <int WS, int NB, bool HAS_MASK, int RB, int FM>
+__global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p, const DecodeInputs in) {
+    constexpr bool FUSED = FM >= 0;
     static_assert(WS == 2 || WS == 4 || WS == 8, "the wave merge is a binary tree");
     static_assert(RB == 1 || RB == 2, "16 or 32 rows");
     constexpr int PER = 8 + (HAS_MASK ? 1 : 0);           // DMA loads per stage
@@ -62,6 +66,10 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
     __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
+    // fused inputs: 1 KiB slots of q_w, k_w, the new token's k and v rows
+    // for this kv head (512 bytes each), its position and its cache row
+    constexpr int kPieces = 6;
+    __shared__ __attribute__((aligned(1024))) char fin[FUSED ? kPieces * 1024 : 16];
     prefetch_params(p);
     int & s_last = *(int *) qlds;                         // after the prologue the query rows are dead
 
@@ -172,12 +180,72 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r2 & 15))) & 31) * 16, lds_addr(qlds) + (uint32_t) (i * 1024));
         }
     }
+    // fused: the weights, this kv head's new K / V rows, the position and
+    // the cache row travel the same way (piece i by wave i % WS)
+    if constexpr (FUSED) {
+        for (int i = ws; i < kPieces; i += WS) {
+            const char * src;
+            uint32_t bytes = 512;
+            if (i == 0) src = in.q_w;
+            else if (i == 1) src = in.k_w;
+            else if (i == 2) src = in.k + kvh * in.k_nb1;
+            else if (i == 3) src = in.v + kvh * 512;
+            else if (i == 4) { src = (const char *) in.pos; bytes = 4; }
+            else { src = in.rows; bytes = (uint32_t) in.rows_nb0; }
+            if (src) dma16(raw_desc(src, bytes), (uint32_t) lane * 16, lds_addr(fin) + (uint32_t) (i * 1024));
+        }
+    }
 #pragma unroll
     for (int u = 0; u < NB - 1; ++u)
         if (u < my_ns) issue(u, u);
     // own query rows landed (the stages were issued after them), then everyone's
     wait_later<NB - 1, PER>(min(NB - 1, my_ns));
     __syncthreads();
+
+    // fused: this wave's query rows through RMSNorm, weight and rotation in
+    // place; the new tokens' K (normed, rotated) and V rows of this kv head,
+    // f16, for the wave whose stage holds the token's cell (it patches the
+    // stage) and for split 0's wave 0 (it writes the cache)
+    int cell_0 = -1;                                                   // the new cell, -1 if out of range
+    int j_own = -1;                                                    // this wave's stage that holds it
+    int64_t row_0 = 0;
+    half2v kvk = {0, 0}, kvv = {0, 0};
+    if constexpr (FUSED) {
+        const int d0 = rope_d0<FM>(lane), d1 = rope_d1<FM>(lane);
+        const int32_t pos_0 = __builtin_amdgcn_readfirstlane(*(const int32_t *) (fin + 4 * 1024));
+        const uint32_t rlo = __builtin_amdgcn_readfirstlane(*(const uint32_t *) (fin + 5 * 1024));
+        const uint32_t rhi = __builtin_amdgcn_readfirstlane(*(const uint32_t *) (fin + 5 * 1024 + 4));
+        row_0 = in.rows64 ? (int64_t) (((uint64_t) rhi << 32) | rlo) : (int64_t) (int32_t) rlo;
+        float cos_0, sin_0;
+        rope_cos_sin<FM>(in.rope, pos_0, lane, cos_0, sin_0);
+        const float * qw = (const float *) fin;
+        const float * kw = (const float *) (fin + 1024);
+        const bool has_qw = in.q_w != nullptr, has_kw = in.k_w != nullptr;
+        const float qw0 = has_qw ? qw[d0] : 1.0f, qw1 = has_qw ? qw[d1] : 1.0f;
+        for (int r = ws; r < rows_here; r += WS) {
+            char * row = qlds + r * 512;
+            float * x0p = (float *) (row + (((d0 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d0 & 3) * 4);
+            float * x1p = (float *) (row + (((d1 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d1 & 3) * 4);
+            float y0, y1;
+            norm_rope_apply<FM>(*x0p, *x1p, has_qw, qw0, qw1, in.eps, cos_0, sin_0, y0, y1);
+            *x0p = y0;
+            *x1p = y1;
+        }
+        cell_0 = row_0 >= 0 && row_0 < in.n_rows ? (int) row_0 : -1;
+        const int rel = cell_0 - c_begin;
+        if (cell_0 >= 0 && rel >= 0 && cell_0 < c_end && rel % sstride < kSC && (rel / sstride) % WS == ws)
+            j_own = (rel / sstride) / WS;
+        if (j_own >= 0 || (split == 0 && ws == 0)) {
+            const float kw0 = has_kw ? kw[d0] : 1.0f, kw1 = has_kw ? kw[d1] : 1.0f;
+            const float * kr = (const float *) (fin + 2 * 1024);
+            const float * vr = (const float *) (fin + 3 * 1024);
+            float y0, y1;
+            norm_rope_apply<FM>(kr[d0], kr[d1], has_kw, kw0, kw1, in.eps, cos_0, sin_0, y0, y1);
+            kvk = half2v{(_Float16) y0, (_Float16) y1};
+            kvv = half2v{(_Float16) vr[d0], (_Float16) vr[d1]};
+        }
+        __syncthreads();                                               // every query row ready
+    }
 
     // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
     half8 qf[RB][4];
@@ -234,6 +302,19 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             mem_barrier();
             const char * st = &lds[ws][u][0];
             const int cs = c_begin + sstride * (ws + j * WS);
+            if constexpr (FUSED) {
+                // the new token's rows replace the cache's copy of its cell
+                // (granule j of cell c at slot j ^ c)
+                if (j == j_own) {
+                    const int c = cell_0 - cs;
+                    const int d0 = rope_d0<FM>(lane), d1 = rope_d1<FM>(lane);
+                    char * sw = &lds[ws][u][0] + c * 256;
+                    *(_Float16 *) (sw + (((d0 >> 3) ^ c) << 4) + (d0 & 7) * 2) = kvk[0];
+                    *(_Float16 *) (sw + (((d1 >> 3) ^ c) << 4) + (d1 & 7) * 2) = kvk[1];
+                    *(_Float16 *) (sw + 4096 + (((d0 >> 3) ^ c) << 4) + (d0 & 7) * 2) = kvv[0];
+                    *(_Float16 *) (sw + 4096 + (((d1 >> 3) ^ c) << 4) + (d1 & 7) * 2) = kvv[1];
+                }
+            }
             u32x4 kf[4];
 #pragma unroll
             for (int kb = 0; kb < 4; ++kb) kf[kb] = *(const u32x4 *) (st + kread + (((4 * kb + g) ^ n) << 4));
@@ -324,6 +405,37 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) l_run[rb] = colsum4(l_run[rb]);
+
+    // fused: split 0 stores the rotated query rows (when asked) and the new
+    // token's K / V rows into the cache; a row out of range is not written
+    // and is reported as set_rows reports it
+    if constexpr (FUSED) {
+        if (split == 0) {
+            const int d0 = rope_d0<FM>(lane), d1 = rope_d1<FM>(lane);
+            if (in.q_out) {
+                for (int r = ws; r < rows_here; r += WS) {
+                    const int t = div_g(r, p.G, p.g_magic);
+                    const int hq = kvh * p.G + r - t * p.G;
+                    const char * row = qlds + r * 512;
+                    float * qo = (float *) (in.q_out + (int64_t) hq * in.qo_nb1 + (int64_t) t * in.qo_nb2);
+                    qo[d0] = *(const float *) (row + (((d0 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d0 & 3) * 4);
+                    qo[d1] = *(const float *) (row + (((d1 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d1 & 3) * 4);
+                }
+            }
+            if (ws == 0) {
+                if (cell_0 < 0) {
+                    if (lane == 0 && atomicCAS(p.err, 0, 1) == 0) p.err[1] = (int) row_0;
+                } else {
+                    _Float16 * kc = (_Float16 *) (in.k_cache + (int64_t) cell_0 * in.kc_nb1) + kvh * 128;
+                    _Float16 * vc = (_Float16 *) (in.v_cache + (int64_t) cell_0 * in.vc_nb1) + kvh * 128;
+                    kc[d0] = kvk[0];
+                    kc[d1] = kvk[1];
+                    vc[d0] = kvv[0];
+                    vc[d1] = kvv[1];
+                }
+            }
+        }
+    }
 
     // merge the WS waves through LDS records [slot][row][132] (the rings are
     // free once every wave is past its loop)
@@ -493,8 +605,20 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 template <int WS, int NB>
 hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
     const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
-    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true, 1>), grid, dim3(WS * 64), 0, stream, p);
-    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1>), grid, dim3(WS * 64), 0, stream, p);
+    const DecodeInputs none = {};
+    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    return hipGetLastError();
+}
+
+template <int WS, int NB>
+hipError_t launch_fused(const FattnParams & p, const DecodeInputs & in, const int mode, hipStream_t stream) {
+    const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, 1);
+    switch (mode) {
+        case 2: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 2>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        case 1: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 1>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        default: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 0>), grid, dim3(WS * 64), 0, stream, p, in); break;
+    }
     return hipGetLastError();
 }
 
@@ -516,8 +640,9 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
         // 17..32 rows: two row blocks, 8 waves x 2 stages
         if (p.R > 32 || waves != 8 || stages != 2) return hipErrorInvalidValue;
         const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
-        if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, true, 2>), grid, dim3(8 * 64), 0, stream, p);
-        else        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2>), grid, dim3(8 * 64), 0, stream, p);
+        const DecodeInputs none = {};
+        if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, true, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
+        else        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
         return hipGetLastError();
     }
     switch (waves * 10 + stages) {
@@ -528,4 +653,15 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
         case 82: return launch_cfg<8, 2>(p, stream);
         default: return hipErrorInvalidValue;
     }
+}
+
+bool fattn_decode_fused_ok(int waves, int stages) { return (waves == 2 && stages == 3) || (waves == 8 && stages == 2); }
+
+hipError_t fattn_decode_launch_fused(const FattnParams & p, const DecodeInputs & in, int mode, int waves, int stages,
+                                     hipStream_t stream) {
+    if (p.R > 16 || p.B != 1 || p.mask || in.T != 1 || mode < 0 || mode > 2)
+        return hipErrorInvalidValue;
+    if (waves == 2 && stages == 3) return launch_fused<2, 3>(p, in, mode, stream);
+    if (waves == 8 && stages == 2) return launch_fused<8, 2>(p, in, mode, stream);
+    return hipErrorInvalidValue;
 }

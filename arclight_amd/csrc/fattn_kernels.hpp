@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "norm_rope.hpp"
+
 // Everything a flash-attention kernel needs, resolved on the host from the
 // al_fattn_args descriptors. Byte strides; pointers are device pointers.
 struct FattnParams {
@@ -65,6 +67,36 @@ constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row ti
 // combinations exist. At most kFattnMaxSplit splits per (stream, kv head);
 // arrival counters as the split-KV kernel's (one per stream x kv head).
 bool fattn_decode_config_ok(int waves, int stages);
+
+// The attention inputs of one layer folded into the decode kernel
+// (al_fattn_f16_with_inputs), for one new token: every workgroup brings its
+// kv head's query rows through RMSNorm, the weight and the rotation itself,
+// and the token's K (normed, rotated) and V rows, rounded to f16, replace
+// the cache's copy of its cell in the stage that holds it; split 0 writes
+// those rows into the cache and, when asked, the query rows into q_out.
+struct DecodeInputs {
+    const char * q_w;                           // f32 [128] or null (ATTN_Q_NORM)
+    const char * k;  int64_t k_nb1, k_nb2;      // f32 rows (kv head, token)
+    const char * k_w;                           // f32 [128] or null (ATTN_K_NORM)
+    const char * v;  int64_t v_nb1;             // f32 [Hkv * 128, T]: token stride
+    const int32_t * pos;                        // [T] positions (rotation)
+    const char * rows; int64_t rows_nb0;        // [T] cache row of each token, i64 or i32
+    int32_t rows64;
+    int32_t T;                                  // 1
+    char * q_out; int64_t qo_nb1, qo_nb2;       // f32 rows (head, token), or null
+    char * k_cache; int64_t kc_nb1;             // f16 rows of Hkv * 128
+    char * v_cache; int64_t vc_nb1;
+    int64_t n_rows;                             // cache rows
+    float eps;
+    RopeConsts rope;
+};
+// mode: the rotation (0 none, 1 pairs (2i, 2i + 1), 2 NEOX); only
+// fattn_decode_fused_ok shapes, no mask tensor, one stream, one token.
+bool fattn_decode_fused_ok(int waves, int stages);
+// The checks of al_attn_inputs_f32 and the fused prologue's limits (prologue.hip).
+int attn_inputs_decode(const struct al_attn_inputs_args * a, DecodeInputs * out, int * mode);
+hipError_t fattn_decode_launch_fused(const FattnParams & p, const DecodeInputs & in, int mode, int waves, int stages,
+                                     hipStream_t stream);
 size_t fattn_decode_lds_bytes(int waves, int stages, bool mask);
 hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream);
 

@@ -21,7 +21,9 @@
 #include <cstring>
 
 #include "../../include/arclight_prologue.h"
+#include "fattn_kernels.hpp"
 #include "kv_write.hpp"
+#include "norm_rope.hpp"
 #include "runtime.hpp"
 
 namespace {
@@ -36,67 +38,21 @@ struct NormRopeParams {
     int64_t n_rows_dst;
     int32_t H, T;
     float eps;
-    float theta_scale, freq_scale, ext_factor, corr0, corr1, mscale;
+    RopeConsts rope;
     int * err;                                     // [2]: first out-of-range cache row
 };
-
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
 
 // Row (head h, token t), one wavefront. MODE: 0 no rotation, 1 pairs
 // (2i, 2i + 1), 2 NEOX pairs (i, i + 64).
 template <int MODE, bool CACHE>
 __device__ __forceinline__ void norm_rope_row(const NormRopeParams & p, const int h, const int t, const int lane) {
-    // every product and sum rounded on its own, as the reference's C source
-    // reads: at angles of thousands of radians one ulp of theta moves the
-    // output by ~1e-4, so a fused multiply-add there would not match
-#pragma clang fp contract(off)
     if (h >= p.H) return;
-
-    const int d0 = MODE == 1 ? 2 * lane : lane;
-    const int d1 = MODE == 1 ? 2 * lane + 1 : lane + 64;
-
-    // cos / sin of pair `lane` at this token's position (ops.cpp:743-772)
-    float c = 1.0f, s = 0.0f;
-    if constexpr (MODE != 0) {
-        const float theta_extrap0 = (float) p.pos[t];
-        float theta_extrap = theta_extrap0;
-        for (int k = 0; k < 63; ++k)
-            if (k < lane) theta_extrap *= p.theta_scale;
-        const float theta_interp = p.freq_scale * theta_extrap;
-        float theta = theta_interp;
-        if (p.ext_factor != 0.0f) {
-            const float yv = ((float) lane - p.corr0) / fmaxf(0.001f, p.corr1 - p.corr0);
-            const float ramp = 1.0f - fminf(1.0f, fmaxf(0.0f, yv));
-            const float mix = ramp * p.ext_factor;
-            theta = theta_interp * (1.0f - mix) + theta_extrap * mix;
-        }
-        c = cosf(theta) * p.mscale;
-        s = sinf(theta) * p.mscale;
-    }
+    const int d0 = rope_d0<MODE>(lane), d1 = rope_d1<MODE>(lane);
     const float w0 = p.w ? p.w[d0] : 1.0f;
     const float w1 = p.w ? p.w[d1] : 1.0f;
-
     const float * xr = (const float *) (p.x + (int64_t) h * p.x_nb1 + (int64_t) t * p.x_nb2);
-    const float x0 = xr[d0];
-    const float x1 = xr[d1];
-    const float sq0 = x0 * x0, sq1 = x1 * x1;
-    const double sum = wave_sum((double) sq0 + (double) sq1);
-    const float mean = (float) (sum / 128.0);
-    const float scale = 1.0f / sqrtf(mean + p.eps);
-    float n0 = x0 * scale, n1 = x1 * scale;
-    if (p.w) {
-        n0 = n0 * w0;
-        n1 = n1 * w1;
-    }
-    float y0 = n0, y1 = n1;
-    if constexpr (MODE != 0) {
-        y0 = n0 * c - n1 * s;
-        y1 = n0 * s + n1 * c;
-    }
+    float y0, y1;
+    norm_rope_pair<MODE>(xr[d0], xr[d1], p.w != nullptr, w0, w1, p.eps, p.rope, MODE != 0 ? p.pos[t] : 0, lane, y0, y1);
     if constexpr (CACHE) {
         const char * ip = p.rows + (int64_t) t * p.rows_nb0;
         const int64_t r = p.rows64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
@@ -172,15 +128,15 @@ int norm_rope_params(const al_tensor * x, const al_tensor * w, const al_tensor *
         else if (rope->mode == AL_ROPE_NORMAL) mode = 1;
         else return al_fail(AL_ERR_UNSUPPORTED, "rms_norm_rope: rope mode %d", rope->mode);
         // host-side constants exactly as the reference's rope op computes them
-        p.theta_scale = powf(rope->freq_base, -2.0f / rope->n_dims);
+        p.rope.theta_scale = powf(rope->freq_base, -2.0f / rope->n_dims);
         const float start = floorf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_fast, rope->freq_base));
         const float end = ceilf(yarn_corr_dim(rope->n_dims, rope->n_ctx_orig, rope->beta_slow, rope->freq_base));
-        p.corr0 = fmaxf(0.0f, start);
-        p.corr1 = fminf((float) (rope->n_dims - 1), end);
-        p.freq_scale = rope->freq_scale;
-        p.ext_factor = rope->ext_factor;
-        p.mscale = rope->attn_factor;
-        if (rope->ext_factor != 0.0f) p.mscale *= 1.0f + 0.1f * logf(1.0f / rope->freq_scale);
+        p.rope.corr0 = fmaxf(0.0f, start);
+        p.rope.corr1 = fminf((float) (rope->n_dims - 1), end);
+        p.rope.freq_scale = rope->freq_scale;
+        p.rope.ext_factor = rope->ext_factor;
+        p.rope.mscale = rope->attn_factor;
+        if (rope->ext_factor != 0.0f) p.rope.mscale *= 1.0f + 0.1f * logf(1.0f / rope->freq_scale);
     }
     p.x = (const char *) x->data; p.x_nb1 = (int64_t) x->nb[1]; p.x_nb2 = (int64_t) x->nb[2];
     p.w = w ? (const float *) w->data : nullptr;
@@ -214,6 +170,51 @@ int norm_rope_params(const al_tensor * x, const al_tensor * w, const al_tensor *
 }
 
 }  // namespace
+
+// The checks of al_attn_inputs_f32, then what the decode kernel needs to fold
+// the inputs into its prologue (one token, operands it can move by 16-byte
+// DMA); fills *out and the rotation mode.
+int attn_inputs_decode(const al_attn_inputs_args * a, DecodeInputs * out, int * mode_out) {
+    if (!a) return al_fail(AL_ERR_INVALID, "attn_inputs: null arguments");
+    NormRopeParams q, k;
+    int mq = 0, mk = 0;
+    int rc = norm_rope_params(&a->q, a->q_w.data ? &a->q_w : nullptr, &a->pos, a->eps, a->rope, &a->q_out, nullptr, &q, &mq);
+    if (rc != AL_OK) return rc;
+    rc = norm_rope_params(&a->k, a->k_w.data ? &a->k_w : nullptr, &a->pos, a->eps, a->rope, &a->k_cache, &a->rows, &k, &mk);
+    if (rc != AL_OK) return rc;
+    if (q.T != k.T) return al_fail(AL_ERR_INVALID, "attn_inputs: q has %d tokens, k %d", q.T, k.T);
+    if (a->v.ne[1] != q.T || a->v.ne[2] != 1 || a->v.ne[3] != 1)
+        return al_fail(AL_ERR_INVALID, "attn_inputs: v must be f32 [n, T] with the tokens of q");
+    SetRowsParams v;
+    bool empty = false;
+    rc = set_rows_params(&a->v_cache, &a->v, &a->rows, &v, &empty);
+    if (rc != AL_OK) return rc;
+    if (empty) return al_fail(AL_ERR_INVALID, "attn_inputs: empty v");
+    auto al16 = [](const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; };
+    const int64_t esz = k.rows64 ? 8 : 4;
+    if (q.T != 1 || v.nc != 128 * k.H || v.n_dst != k.n_rows_dst || k.rows_nb0 != esz ||
+        !al16(k.x) || k.x_nb1 % 16 || k.x_nb2 % 16 || !al16(v.src) || v.s_nb1 % 16 || !al16(k.rows) || !al16(k.pos) ||
+        (q.w && !al16(q.w)) || (k.w && !al16(k.w)))
+        return al_fail(AL_ERR_UNSUPPORTED, "attn_inputs: operands the fused decode prologue cannot take");
+    DecodeInputs d;
+    memset(&d, 0, sizeof(d));
+    d.q_w = (const char *) q.w;
+    d.k = k.x; d.k_nb1 = k.x_nb1; d.k_nb2 = k.x_nb2;
+    d.k_w = (const char *) k.w;
+    d.v = v.src; d.v_nb1 = v.s_nb1;
+    d.pos = q.pos;
+    d.rows = k.rows; d.rows_nb0 = k.rows_nb0; d.rows64 = k.rows64;
+    d.T = q.T;
+    d.q_out = q.y; d.qo_nb1 = q.y_nb1; d.qo_nb2 = q.y_nb2;
+    d.k_cache = k.y; d.kc_nb1 = k.y_nb1;
+    d.v_cache = v.dst; d.vc_nb1 = v.d_nb1;
+    d.n_rows = k.n_rows_dst;
+    d.eps = a->eps;
+    d.rope = q.rope;
+    *out = d;
+    *mode_out = mq;
+    return AL_OK;
+}
 
 extern "C" int al_rms_norm_rope_f32(const al_tensor * x, const al_tensor * w, const al_tensor * pos, float eps,
                                     const al_rope_params * rope, const al_tensor * y, const al_tensor * rows,

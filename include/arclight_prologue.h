@@ -93,6 +93,25 @@ typedef struct al_attn_inputs_args {
 
 int al_attn_inputs_f32(const al_attn_inputs_args * a, void * stream);
 
+/*
+ * al_fattn_f16 with the layer's attention inputs folded into the decode
+ * kernel: the same results, bit for bit, as al_attn_inputs_f32(in,
+ * a->stream) followed by al_fattn_f16(a), in one launch (q_out and the K / V
+ * cache rows are written as that pair writes them). No single counterpart
+ * in the reference, which runs rms_norm -> mul -> rope_ext for Q and K,
+ * cpy_k / cpy_v and flash_attn_ext as separate nodes
+ * (models/qwen3.cpp:211-227, nnml/src/cgraph.cpp:485-488); it takes the
+ * inputs' launch out of a decode step. a->q must view in->q_out (the query
+ * rows the inputs produce), a->k and a->v the caches in->k_cache and
+ * in->v_cache (cell c = cache row c, heads of 128 halves). A call that does
+ * not run on the decode kernel (more than 16 query rows per kv head, a mask
+ * tensor, several streams), has more than one token, or whose operands the fused
+ * prologue cannot move (16-byte aligned rows and indices) returns
+ * AL_ERR_UNSUPPORTED before anything is enqueued; the pair of calls then
+ * does the same work.
+ */
+int al_fattn_f16_with_inputs(const al_attn_inputs_args * in, const al_fattn_args * a);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,10 +30,11 @@ def _case(name):
     print(f"\n[case] {name}", flush=True)
 
 
-@pytest.mark.parametrize("one_launch_inputs", [False, True])
-def test_decode_loop_graph_replay(gpu, one_launch_inputs):
-    """one_launch_inputs: Q, K and V of a layer through al_attn_inputs_f32
-    instead of the three separate ops."""
+@pytest.mark.parametrize("inputs", ["separate", "one_launch", "fused"])
+def test_decode_loop_graph_replay(gpu, inputs):
+    """inputs: Q, K and V of a layer as three separate ops, through
+    al_attn_inputs_f32 (one launch), or folded into the attention launch
+    (al_fattn_f16_with_inputs)."""
     from arclight_amd import device, fattn, kv, matmul, prologue
     Hq, Hkv, D, L, N = 32, 8, 128, 2, 2560
     K = Hq * D
@@ -80,17 +81,24 @@ def test_decode_loop_graph_replay(gpu, one_launch_inputs):
 
     def enqueue_step():
         for il in range(L):
-            if one_launch_inputs:
-                prologue.attn_inputs(d_qc, d_wq[il], d_kc, d_wk[il], d_vc, d_pos, d_row, d_q[il],
-                                     ring.cache_rows(il, "k"), ring.cache_rows(il, "v"), eps=EPS, rope=rope, stream=stream)
+            if inputs == "fused":
+                prologue.attention_with_inputs(d_qc, d_wq[il], d_kc, d_wk[il], d_vc, d_pos, d_row, d_q[il],
+                                               ring.cache_rows(il, "k"), ring.cache_rows(il, "v"), ring.get_k(il, NKV),
+                                               ring.get_v(il, NKV), d_att[il], eps=EPS, scale=scale, rope=rope,
+                                               kv_len=NKV, causal_pos0=0, dyn_len=d_dyn, stream=stream)
             else:
-                prologue.rms_norm_rope(d_qc, d_wq[il], d_pos, eps=EPS, rope=rope, y=d_q[il], stream=stream)
-                prologue.rms_norm_rope(d_kc, d_wk[il], d_pos, eps=EPS, rope=rope, y=ring.cache_rows(il, "k"),
-                                       rows=d_row, stream=stream)
-                fattn.set_rows(ring.cache_rows(il, "v"), d_vc, d_row, stream=stream)
-            qv = device.DeviceTensor(d_q[il].buf, abi.AL_TYPE_F32, (1, 1, Hq, D), None, 0, abi.Q_AXES)
-            fattn.flash_attn_ext(qv, ring.get_k(il, NKV), ring.get_v(il, NKV), scale=scale, dst=d_att[il],
-                                 kv_len=NKV, causal_pos0=0, stream=stream, dyn_len=d_dyn)
+                if inputs == "one_launch":
+                    prologue.attn_inputs(d_qc, d_wq[il], d_kc, d_wk[il], d_vc, d_pos, d_row, d_q[il],
+                                         ring.cache_rows(il, "k"), ring.cache_rows(il, "v"), eps=EPS, rope=rope,
+                                         stream=stream)
+                else:
+                    prologue.rms_norm_rope(d_qc, d_wq[il], d_pos, eps=EPS, rope=rope, y=d_q[il], stream=stream)
+                    prologue.rms_norm_rope(d_kc, d_wk[il], d_pos, eps=EPS, rope=rope, y=ring.cache_rows(il, "k"),
+                                           rows=d_row, stream=stream)
+                    fattn.set_rows(ring.cache_rows(il, "v"), d_vc, d_row, stream=stream)
+                qv = device.DeviceTensor(d_q[il].buf, abi.AL_TYPE_F32, (1, 1, Hq, D), None, 0, abi.Q_AXES)
+                fattn.flash_attn_ext(qv, ring.get_k(il, NKV), ring.get_v(il, NKV), scale=scale, dst=d_att[il],
+                                     kv_len=NKV, causal_pos0=0, stream=stream, dyn_len=d_dyn)
             x = device.DeviceTensor(d_att[il].buf, abi.AL_TYPE_F32, (1, K))
             matmul.mul_mat_q4_0(d_wo[il], x, d_y[il], stream)
 
@@ -98,7 +106,7 @@ def test_decode_loop_graph_replay(gpu, one_launch_inputs):
     try:
         for s in range(STEPS):
             p = P0 + s
-            how = ("eager" if s == 0 else "graph replay") + (", one-launch inputs" if one_launch_inputs else "")
+            how = ("eager" if s == 0 else "graph replay") + f", inputs {inputs}"
             _case(f"graph decode: step {s} at position {p} ({how})")
             rows, n_kv = ring.cells.place([(p, [0])])
             assert n_kv <= NKV and ring.cells.implicit([(p, [0])], n_kv) == (p + 1, p)
