@@ -168,8 +168,9 @@ struct Plan {
     int waves = 2;                  // decode kernel: wavefronts per workgroup
     int stages = 2;                 // decode kernel: LDS stage buffers
     int rows_per_tile = 16;
-    size_t counters_bytes = 0;
+    size_t part_offset = 0;         // merge records: workspace offset and bytes (0: none)
     size_t part_bytes = 0;
+    size_t workspace_bytes() const { return part_bytes ? part_offset + part_bytes : 0; }
 };
 
 bool aligned16(const void * ptr) { return ((uintptr_t) ptr & 15u) == 0; }
@@ -256,6 +257,11 @@ bool decode_interleave() {
 }
 int decode_min_stages() {
     static int v = env_int("AL_DECODE_MIN_STAGES", 2);
+    return v;
+}
+// Most splits per (stream, kv head) (AL_DECODE_MAX_SPLIT, at most kFattnMaxSplit).
+int decode_max_split() {
+    static int v = std::min(env_int("AL_DECODE_MAX_SPLIT", kFattnMaxSplit), kFattnMaxSplit);
     return v;
 }
 
@@ -391,7 +397,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.split_magic = magic_u32(prefill_split * in_wg_split);
         p.tiles_magic = magic_u32(prefill_tiles);
         if (prefill_split > 1) {
-            pl.counters_bytes = kFattnCounterBytes;
+            pl.part_offset = kFattnCounterBytes;
             pl.part_bytes = prefill_part;
         }
         *out = pl;
@@ -438,13 +444,15 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         int64_t n_split = (target + decode_units - 1) / decode_units;
         // every wave of a split gets at least decode_min_stages() stages
         n_split = std::min<int64_t>(n_split, std::max<int64_t>(1, nst / (dwaves * decode_min_stages())));
-        n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, kFattnMaxSplit));
+        n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, decode_max_split()));
+        // split flags: kFattnMaxSplit counter words per unit
+        if (decode_units * kFattnMaxSplit > kFattnCounterWords) n_split = 1;
         const int64_t cps = (nst + n_split - 1) / n_split;
         p.cells_per_split = (int32_t) (cps * 16);
         p.n_split = (int32_t) ((nst + cps - 1) / cps);
         p.interleave = decode_interleave() ? 1 : 0;
         if (p.n_split > 1) {
-            pl.counters_bytes = kFattnCounterBytes;
+            pl.part_offset = kFattnCounterBytes;
             pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
         }
         *out = pl;
@@ -474,7 +482,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
     if (n_split == 1) p.cells_per_split = (int32_t) std::max<int64_t>(32, (extent + 31) / 32 * 32);
     p.n_split = (int32_t) n_split;
     if (p.n_split > 1) {
-        pl.counters_bytes = kFattnCounterBytes;
+        pl.part_offset = kFattnCounterBytes;
         pl.part_bytes = (size_t) units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
     }
     *out = pl;
@@ -488,7 +496,7 @@ extern "C" uint64_t al_fattn_workspace_bytes(const al_fattn_args * a) {
     if (al_device_cu_count(&n_cu) != AL_OK || al_device_lds_per_block(&lds) != AL_OK) return 0;
     Plan pl;
     if (make_plan(a, n_cu, lds, &pl) != AL_OK) return 0;
-    return pl.counters_bytes + pl.part_bytes;
+    return pl.workspace_bytes();
 }
 
 // One call with the plan's workspace: the caller's, else the library's for
@@ -510,7 +518,7 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
                   pl.p.B != 1 || pl.p.mask))
         return al_fail(AL_ERR_UNSUPPORTED, "fattn_with_inputs: the call does not run on the decode kernel "
                        "(up to 16 rows per kv head, one stream, no mask tensor)");
-    const size_t need = pl.counters_bytes + pl.part_bytes;
+    const size_t need = pl.workspace_bytes();
     if (need) {
         void * ws = noalloc_ws ? noalloc_ws : a->workspace;
         if (noalloc_ws) {
@@ -526,7 +534,7 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
             if (rc != AL_OK) return rc;
         }
         pl.p.counters = (unsigned *) ws;
-        pl.p.part = (float *) ((char *) ws + pl.counters_bytes);
+        pl.p.part = (float *) ((char *) ws + pl.part_offset);
     }
     rc = al_device_error_flag(&pl.p.err);
     if (rc != AL_OK) return rc;
@@ -641,7 +649,7 @@ extern "C" int al_device_errors(void) {
         e = hipMemset(flag, 0, sizeof(h));
         if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
         if (h[0]) return al_fail(AL_ERR_INVALID, "set_rows: row index %d out of range (ops.cpp:171)", h[1]);
-        return al_fail(AL_ERR_HIP, "fattn prefill: a wave gave up waiting for its partner's tile hand-off");
+        return al_fail(AL_ERR_HIP, "fattn decode: a merging workgroup gave up waiting for the other splits' records");
     }
     return AL_OK;
 }

@@ -71,6 +71,13 @@ __device__ __forceinline__ unsigned add_agent(unsigned * p, unsigned v) {
 __device__ __forceinline__ void st_agent_u32(unsigned * p, unsigned v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ unsigned ld_agent_u32(const unsigned * p) {
+    return __hip_atomic_load(const_cast<unsigned *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Polls of a merging workgroup for the split flags of its launch before it
+// gives up and reports it (each poll a round trip to the coherence point
+// after a short sleep: about a second in all).
+constexpr int kFlagPollLimit = 1 << 20;
 // Keeps the compiler from moving this wave's memory accesses across it and
 // waits until all of them have completed (s_waitcnt 0).
 __device__ __forceinline__ void complete_wave_memops() {

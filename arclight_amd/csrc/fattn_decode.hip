@@ -71,7 +71,6 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     constexpr int kPieces = 6;
     __shared__ __attribute__((aligned(1024))) char fin[FUSED ? kPieces * 1024 : 16];
     prefetch_params(p);
-    int & s_last = *(int *) qlds;                         // after the prologue the query rows are dead
 
     const int lane = threadIdx.x & 63;
     const int ws = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -494,30 +493,54 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         return;
     }
 
-    // publish this split's record: [unit][split][row][132]
+    // Publish this split's record [unit][split][row][132] and then, once its
+    // stores have completed, the split's flag (one word per split of the
+    // unit, all in one 128-byte line of the counter region, zero between
+    // calls). One split of each unit merges: it polls the flag line until
+    // every split has set its word, then reads each record once. (Re-reading
+    // lines device-coherently is slow, so the records are never polled; and
+    // no split waits on a shared arrival counter, whose updates from all
+    // splits serialize.) The merging split is n_split - 1 - unit % 8, so that
+    // the units' mergers, and their polling, fall on different XCDs
+    // (workgroup ids go round the XCDs, split fastest). A merger waits only
+    // for workgroups of its own unit, which on every XCD are dispatched
+    // ahead of any later unit's, so it always has workgroups to wait for that
+    // can run; its polls are bounded anyway (kFlagPollLimit).
     constexpr uint32_t RS = REC * 4;                                   // bytes of one split's record
     const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * REC, RS * (uint32_t) p.n_split);
+    unsigned * flags = p.counters + unit * kMaxSplit;
+    if (ws == 0) {
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-        if (ws == 0 && rvalid[rb]) {
-            const uint32_t row = (uint32_t) split * RS + (uint32_t) ((16 * rb + n) * kRowStride * 4);
+        for (int rb = 0; rb < RB; ++rb) {
+            if (rvalid[rb]) {
+                const uint32_t row = (uint32_t) split * RS + (uint32_t) ((16 * rb + n) * kRowStride * 4);
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb)
-                buf_store16_dev(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]}, pr,
-                                row + (16 * mb + 4 * g) * 4);
-            if (g == 0) buf_store8_dev(float2{m_run[rb], l_run[rb]}, pr, row + 128 * 4);
+                for (int mb = 0; mb < 8; ++mb)
+                    buf_store16_dev(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]}, pr,
+                                    row + (16 * mb + 4 * g) * 4);
+                if (g == 0) buf_store8_dev(float2{m_run[rb], l_run[rb]}, pr, row + 128 * 4);
+            }
         }
+        complete_wave_memops();
+        if (lane == 0) st_agent_u32(flags + split, 1u);
     }
-    complete_wave_memops();
+    if (split != p.n_split - 1 - unit % min(8, p.n_split)) return;
+    if (ws == 0) {
+        for (int tries = 0;; ++tries) {
+            const unsigned f = lane < p.n_split ? ld_agent_u32(flags + lane) : 1u;
+            if (__all(f != 0u)) break;
+            if (tries >= kFlagPollLimit) {
+                if (lane == 0) atomicCAS(p.err + 2, 0, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        order_after_counter();
+        if (lane < p.n_split) st_agent_u32(flags + lane, 0u);         // zero again for the next call in stream order
+    }
     __syncthreads();
-    unsigned * cnt = p.counters + unit;
-    if (threadIdx.x == 0) s_last = (add_agent(cnt, 1u) == (unsigned) (p.n_split - 1));
-    __syncthreads();
-    if (!s_last) return;
-    order_after_counter();
-    if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
 
-    // Last workgroup. The (m, l) pair of every (row, split) is loaded once
+    // The merge. The (m, l) pair of every (row, split) is loaded once
     // (thread i takes pairs i, i + 64 WS, ...) and shared through LDS; the
     // output items are two adjacent lanes per (row, 4 dims), each taking 16
     // of the at most 32 splits and then combining with its partner (split

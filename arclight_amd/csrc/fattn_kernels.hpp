@@ -65,7 +65,9 @@ constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row ti
 // workgroup, `waves` wavefronts each streaming 16-cell stages of K/V through
 // a private ring of `stages` LDS buffers; fattn_decode_config_ok tells which
 // combinations exist. At most kFattnMaxSplit splits per (stream, kv head);
-// arrival counters as the split-KV kernel's (one per stream x kv head).
+// with more than one, merge records in the workspace and one flag word per
+// split in its counter region (kFattnMaxSplit words per stream x kv head);
+// the last split of each (stream, kv head) merges.
 bool fattn_decode_config_ok(int waves, int stages);
 
 // The attention inputs of one layer folded into the decode kernel
