@@ -68,7 +68,8 @@ using namespace fattn_prefill;
 constexpr int kTC = 64;                          // cells per tile
 constexpr int kTileBytes = kTC * 256;            // one tile of K or of V (16 KiB)
 static_assert(kLds == 10 * kTileBytes, "10 tiles fill the LDS");
-static_assert(80 * 1024 + 128 * 512 <= kLds && 64 * kFattnRecordStride * 4 <= 80 * 1024, "output staging fits past the merge records");
+static_assert(80 * 1024 + 128 * 512 + 128 * 8 <= kLds - 16 && 64 * kFattnRecordStride * 4 <= 80 * 1024,
+              "output staging fits past the merge records");
 
 // Shape of a workgroup with RG row groups: SP cell splits; per split a ring
 // of NK K buffers and NV V buffers; PER LDS-DMA instructions per wave and
@@ -676,7 +677,9 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     // O^T lane l: row lr, dims 32 db + 8 bq + 4 h .. + 3 in o[db][4 bq .. 4 bq + 3].
     // One workgroup per row tile: the owners put the finished rows into LDS
     // (past the merge records; 16-byte granule g of row r at slot g ^ (r & 31)),
-    // then all threads store whole rows, 16 bytes per lane.
+    // then all threads store whole rows, 16 bytes per lane, non-temporal (the
+    // rows stream to memory instead of waiting in L2 for the end of the
+    // launch: 3 % on 512-token chunks).
     if (p.n_split == 1) {
         float * stage = (float *) (lds + 80 * 1024);
         if (owner && rvalid) {
@@ -697,7 +700,8 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             const int rg_ = row0 + r;
             const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
             float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
-            *(float4 *) (out + 4 * g) = *(const float4 *) (stage + r * 128 + 4 * (g ^ (r & 31)));
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, *(const float4 *) (stage + r * 128 + 4 * (g ^ (r & 31)))),
+                                                   make_rsrc(out, 512), 16 * g, 0, kNonTemporal);
         }
         return;
     }
@@ -705,55 +709,90 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     // Workgroup splits: publish this workgroup's record [unit][sx][row][132]
     // with device-coherent stores; the last workgroup of the row tile to
     // arrive combines the records of all of them (fixed order) into dst.
+    // The record goes out as whole lines: the owners put their rows into LDS
+    // (as the finished rows above), then all threads store consecutive
+    // 16-byte granules of the record, so every write covers whole lines
+    // (a row-per-lane write of 32 bytes to each of 32 rows made every write
+    // partial, and publication took ~4 us).
     const int unit = (b * p.Hkv + kvh) * p.n_row_tiles + rt;
     constexpr uint32_t RS = ROWS * kRowStride * 4;                 // record bytes
+    constexpr int kGran = kRowStride / 4;                          // 16-byte granules per record row
     const rsrc_t rec = make_rsrc(p.part + (int64_t) unit * p.n_split * (ROWS * kRowStride), RS * (uint32_t) p.n_split);
-    if (owner) {
-        const uint32_t row = (uint32_t) sx * RS + (uint32_t) (rr * kRowStride * 4);
+    {
+        float * stage = (float *) (lds + 80 * 1024);
+        float2 * ml_stage = (float2 *) (lds + 80 * 1024 + 128 * 512);
+        if (owner) {
 #pragma unroll
-        for (int db = 0; db < 4; ++db)
+            for (int db = 0; db < 4; ++db)
 #pragma unroll
-            for (int bq = 0; bq < 4; ++bq)
-                buf_store16_dev(float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]}, rec,
-                                row + (uint32_t) ((32 * db + 8 * bq + 4 * h) * 4));
-        if (h == 0) buf_store8_dev(float2{m_nat, l_row}, rec, row + 128 * 4);
+                for (int bq = 0; bq < 4; ++bq) {
+                    const int g = 8 * db + 2 * bq + h;
+                    *(float4 *) (stage + rr * 128 + 4 * (g ^ (rr & 31))) =
+                        float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
+                }
+            if (h == 0) ml_stage[rr] = float2{m_nat, l_row};
+        }
+        __syncthreads();
+        for (int i = threadIdx.x; i < rows_here * kGran; i += 2 * kWaves * 64) {
+            const int r = i / kGran, j = i - r * kGran;
+            const float2 ml = ml_stage[r];
+            const float4 v = j < 32 ? *(const float4 *) (stage + r * 128 + 4 * (j ^ (r & 31))) : float4{ml.x, ml.y, 0.0f, 0.0f};
+            buf_store16_dev(v, rec, (uint32_t) sx * RS + (uint32_t) i * 16);
+        }
     }
     complete_wave_memops();
     __syncthreads();
     unsigned * cnt = p.counters + unit;
-    int * s_last = (int *) (lds + kLds - 16);                       // past the merge rows
+    int * s_last = (int *) (lds + kLds - 16);                       // past the staged rows
     if (threadIdx.x == 0) *s_last = (add_agent(cnt, 1u) == (unsigned) (p.n_split - 1));
     __syncthreads();
     if (!*s_last) return;
     order_after_counter();
     if (threadIdx.x == 0) st_agent_u32(cnt, 0u);                     // ready for the next call in stream order
-    // thread t takes (row, 4 dims) items t, t + kMerge, ...: all records' loads in flight at once
-    for (int item = threadIdx.x; item < rows_here * 32; item += 2 * kWaves * 64) {
-        const int r = item >> 5, d4 = item & 31;
-        float2 ml[kMaxPrefillSplit];
-        float4 ov[kMaxPrefillSplit];
+    // Thread t takes (row, 4 dims) items t, t + 512, ..., kBatch at a time,
+    // with every record's loads of the batch in flight at once (no loads for
+    // splits past n_split).
+    constexpr int kBatch = 4;
+    for (int base = threadIdx.x; base < rows_here * 32; base += kBatch * 2 * kWaves * 64) {
+        float2 ml[kBatch][kMaxPrefillSplit];
+        float4 ov[kBatch][kMaxPrefillSplit];
 #pragma unroll
-        for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
-            const uint32_t row = (uint32_t) min(s2, p.n_split - 1) * RS + (uint32_t) (r * kRowStride * 4);
-            ml[s2] = buf_load8_dev(rec, row + 128 * 4);
-            ov[s2] = buf_load16_dev(rec, row + (uint32_t) (d4 * 16));
+        for (int k = 0; k < kBatch; ++k) {
+            const int item = min(base + k * 2 * kWaves * 64, rows_here * 32 - 1);
+            const int r = item >> 5, d4 = item & 31;
+#pragma unroll
+            for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
+                ml[k][s2] = float2{-AL_INF, 0.0f};
+                ov[k][s2] = float4{0, 0, 0, 0};
+                if (s2 < p.n_split) {
+                    const uint32_t row = (uint32_t) s2 * RS + (uint32_t) (r * kRowStride * 4);
+                    ml[k][s2] = buf_load8_dev(rec, row + 128 * 4);
+                    ov[k][s2] = buf_load16_dev(rec, row + (uint32_t) (d4 * 16));
+                }
+            }
         }
-        float M = ml[0].x;
 #pragma unroll
-        for (int s2 = 1; s2 < kMaxPrefillSplit; ++s2) M = s2 < p.n_split ? fmaxf(M, ml[s2].x) : M;
-        const float Mu = M == -AL_INF ? 0.0f : M;
-        float L = 0.0f;
-        float4 acc = {0, 0, 0, 0};
+        for (int k = 0; k < kBatch; ++k) {
+            const int item = base + k * 2 * kWaves * 64;
+            if (item >= rows_here * 32) break;
+            const int r = item >> 5, d4 = item & 31;
+            float M = ml[k][0].x;
 #pragma unroll
-        for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
-            const float w = s2 < p.n_split ? exp_fast(ml[s2].x - Mu) : 0.0f;
-            L += w * ml[s2].y;
-            acc.x += w * ov[s2].x; acc.y += w * ov[s2].y; acc.z += w * ov[s2].z; acc.w += w * ov[s2].w;
+            for (int s2 = 1; s2 < kMaxPrefillSplit; ++s2) M = fmaxf(M, ml[k][s2].x);
+            const float Mu = M == -AL_INF ? 0.0f : M;
+            float L = 0.0f;
+            float4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int s2 = 0; s2 < kMaxPrefillSplit; ++s2) {
+                const float w = s2 < p.n_split ? exp_fast(ml[k][s2].x - Mu) : 0.0f;
+                L += w * ml[k][s2].y;
+                acc.x += w * ov[k][s2].x; acc.y += w * ov[k][s2].y; acc.z += w * ov[k][s2].z; acc.w += w * ov[k][s2].w;
+            }
+            const int rg_ = row0 + r;
+            const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
+            float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
+            *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
         }
-        const int rg_ = row0 + r;
-        const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
-        float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
-        *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
     }
 }
 

@@ -27,6 +27,9 @@ __device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
 }
 // Device-coherent (sc1) stores / loads of merge records, see st_agent.
 constexpr int kCoherent = 16;
+// Non-temporal (nt) cache policy: output rows that no later access of the
+// launch reads.
+constexpr int kNonTemporal = 2;
 __device__ __forceinline__ void buf_store16_dev(float4 v, rsrc_t r, uint32_t off) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int) off, 0, kCoherent);
 }
