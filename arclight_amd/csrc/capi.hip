@@ -649,7 +649,7 @@ extern "C" int al_device_errors(void) {
         e = hipMemset(flag, 0, sizeof(h));
         if (e != hipSuccess) return al_hip_fail(e, "hipMemset(error flag)");
         if (h[0]) return al_fail(AL_ERR_INVALID, "set_rows: row index %d out of range (ops.cpp:171)", h[1]);
-        return al_fail(AL_ERR_HIP, "fattn decode: a merging workgroup gave up waiting for the other splits' records");
+        return al_fail(AL_ERR_HIP, "fattn: a merging workgroup gave up waiting for the other splits' records");
     }
     return AL_OK;
 }
