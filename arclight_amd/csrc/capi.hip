@@ -453,7 +453,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.interleave = decode_interleave() ? 1 : 0;
         if (p.n_split > 1) {
             pl.part_offset = kFattnCounterBytes;
-            pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kFattnRecordStride * sizeof(float);
+            pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kDecodeRecRow;
         }
         *out = pl;
         return AL_OK;

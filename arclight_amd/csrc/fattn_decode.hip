@@ -506,19 +506,25 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     // for workgroups of its own unit, which on every XCD are dispatched
     // ahead of any later unit's, so it always has workgroups to wait for that
     // can run; its polls are bounded anyway (kFlagPollLimit).
-    constexpr uint32_t RS = REC * 4;                                   // bytes of one split's record
-    const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * REC, RS * (uint32_t) p.n_split);
+    // A split's record holds the O rows of its 16 RB query rows (512 bytes
+    // each), then their (m, l) pairs, so that the pairs share no line with O
+    // and the merger loads every line once (re-reading a line
+    // device-coherently is slow).
+    constexpr uint32_t RS = 16 * RB * kDecodeRecRow;                  // bytes of one split's record
+    constexpr uint32_t kPairs0 = 16 * RB * 512;                       // the pairs' offset in a record
+    const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * (RS / 4), RS * (uint32_t) p.n_split);
     unsigned * flags = p.counters + unit * kMaxSplit;
     if (ws == 0) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             if (rvalid[rb]) {
-                const uint32_t row = (uint32_t) split * RS + (uint32_t) ((16 * rb + n) * kRowStride * 4);
+                const uint32_t row = (uint32_t) split * RS + (uint32_t) ((16 * rb + n) * 512);
 #pragma unroll
                 for (int mb = 0; mb < 8; ++mb)
                     buf_store16_dev(float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]}, pr,
                                     row + (16 * mb + 4 * g) * 4);
-                if (g == 0) buf_store8_dev(float2{m_run[rb], l_run[rb]}, pr, row + 128 * 4);
+                if (g == 0)
+                    buf_store8_dev(float2{m_run[rb], l_run[rb]}, pr, (uint32_t) split * RS + kPairs0 + (uint32_t) ((16 * rb + n) * 8));
             }
         }
         complete_wave_memops();
@@ -560,7 +566,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     for (int i = 0; i < kPairs; ++i) {
         const int pi = i * WS * 64 + threadIdx.x;
         const int rr = min(pi / kMaxSplit, rows_here - 1), sp = min(pi % kMaxSplit, p.n_split - 1);
-        mlv[i] = buf_load8_dev(pr, (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4 + 128 * 4));
+        mlv[i] = buf_load8_dev(pr, (uint32_t) sp * RS + kPairs0 + (uint32_t) (rr * 8));
     }
     const int n_items = rows_here * 64;
     for (int base = 0; base < n_items; base += kItems * WS * 64) {
@@ -574,7 +580,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
                 const int sp = min(half * kHalf + j, p.n_split - 1);
-                ov[it2][j] = buf_load16_dev(pr, (uint32_t) sp * RS + (uint32_t) (rr * kRowStride * 4 + d4 * 16));
+                ov[it2][j] = buf_load16_dev(pr, (uint32_t) sp * RS + (uint32_t) (rr * 512 + d4 * 16));
             }
         }
         if (base == 0) {

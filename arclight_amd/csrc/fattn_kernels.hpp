@@ -104,6 +104,10 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
 
 // Floats of one split-KV merge record row (O[128], m, l, pad).
 constexpr int kFattnRecordStride = 132;
+// Bytes per query row of a decode split's record (O[128] as a block of rows,
+// then the rows' (m, l) pairs): 16 RB rows make a whole number of 128-byte
+// lines.
+constexpr int kDecodeRecRow = 520;
 // At most kFattnMaxSplit splits per row tile; one merge level.
 constexpr int kFattnMaxSplit = 32;
 // Every workspace starts with a fixed arrival-counter region (one counter
