@@ -211,6 +211,18 @@ int prefill_rows_forced() {
     return v;
 }
 
+// Prefill workgroup splits: at most AL_PREFILL_MAX_SPLIT per row tile, and a
+// split only when each workgroup keeps at least AL_PREFILL_SPLIT_TILES 64-cell
+// tiles per in-workgroup split.
+int prefill_max_split() {
+    static int v = std::min(env_int("AL_PREFILL_MAX_SPLIT", kFattnPrefillMaxSplit), kFattnPrefillMaxSplit);
+    return v;
+}
+int prefill_split_tiles() {
+    static int v = env_int("AL_PREFILL_SPLIT_TILES", 4);
+    return v;
+}
+
 int wgs_per_cu() {
     static int v = env_int("AL_SPLITKV_WGS_PER_CU", 2);
     return v;
@@ -257,6 +269,16 @@ bool decode_interleave() {
 }
 int decode_min_stages() {
     static int v = env_int("AL_DECODE_MIN_STAGES", 2);
+    return v;
+}
+// Query rows each merging workgroup of a split decode call takes
+// (AL_DECODE_MERGE_ROWS). A merger is bound by the record bytes its CU
+// loads (32 splits x 520 bytes per row), but every merger polls the same
+// flag line, so few of them: 8 rows each (decode 1 merger, 4-draft verify 2,
+// 8-draft verify 4: 21.7 -> 16.7 us per layer at 8K cells; one per row is
+// slower again).
+int decode_merge_rows() {
+    static int v = env_int("AL_DECODE_MERGE_ROWS", 8);
     return v;
 }
 // Most splits per (stream, kv head) (AL_DECODE_MAX_SPLIT, at most kFattnMaxSplit).
@@ -373,8 +395,8 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         int64_t extent = p.kv_hi;
         if (p.causal_pos0 >= 0) extent = std::min<int64_t>(extent, p.causal_pos0 + T);
         const int64_t cell_tiles = std::max<int64_t>(1, (extent + 63) / 64);
-        while (prefill_split < kFattnPrefillMaxSplit && prefill_units * prefill_split < n_cu &&
-               cell_tiles >= 2 * in_wg_split * (prefill_split + 1))
+        while (prefill_split < prefill_max_split() && prefill_units * prefill_split < n_cu &&
+               cell_tiles >= prefill_split_tiles() * in_wg_split * (prefill_split + 1))
             ++prefill_split;
     }
     // (an explicit mask: the prefill kernel reads its rows 16 bytes at a time)
@@ -445,12 +467,13 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         // every wave of a split gets at least decode_min_stages() stages
         n_split = std::min<int64_t>(n_split, std::max<int64_t>(1, nst / (dwaves * decode_min_stages())));
         n_split = std::max<int64_t>(1, std::min<int64_t>(n_split, decode_max_split()));
-        // split flags: kFattnMaxSplit counter words per unit
-        if (decode_units * kFattnMaxSplit > kFattnCounterWords) n_split = 1;
+        // split flags: kFattnDecodeFlagWords counter words per unit
+        if (decode_units > kFattnDecodeFlagUnits) n_split = 1;
         const int64_t cps = (nst + n_split - 1) / n_split;
         p.cells_per_split = (int32_t) (cps * 16);
         p.n_split = (int32_t) ((nst + cps - 1) / cps);
         p.interleave = decode_interleave() ? 1 : 0;
+        p.merge_rows = decode_merge_rows();
         if (p.n_split > 1) {
             pl.part_offset = kFattnCounterBytes;
             pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kDecodeRecRow;

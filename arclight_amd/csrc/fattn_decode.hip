@@ -493,28 +493,34 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         return;
     }
 
-    // Publish this split's record [unit][split][row][132] and then, once its
-    // stores have completed, the split's flag (one word per split of the
-    // unit, all in one 128-byte line of the counter region, zero between
-    // calls). One split of each unit merges: it polls the flag line until
-    // every split has set its word, then reads each record once. (Re-reading
-    // lines device-coherently is slow, so the records are never polled; and
-    // no split waits on a shared arrival counter, whose updates from all
-    // splits serialize.) The merging split is n_split - 1 - unit % 8, so that
-    // the units' mergers, and their polling, fall on different XCDs
-    // (workgroup ids go round the XCDs, split fastest). A merger waits only
-    // for workgroups of its own unit, which on every XCD are dispatched
-    // ahead of any later unit's, so it always has workgroups to wait for that
-    // can run; its polls are bounded anyway (kFlagPollLimit).
-    // A split's record holds the O rows of its 16 RB query rows (512 bytes
-    // each), then their (m, l) pairs, so that the pairs share no line with O
-    // and the merger loads every line once (re-reading a line
-    // device-coherently is slow).
+    // Publish this split's record and then, once its stores have completed,
+    // the split's flag; K = min(n_split, rows) splits of the unit merge, merger
+    // k taking rows k, k + K, ... (the merge is bound by the record bytes one
+    // CU loads, so it is spread). A split's record holds the O rows of its 16
+    // RB query rows (512 bytes each), then their (m, l) pairs, so that the
+    // pairs share no line with O and every line is loaded once (re-reading a
+    // line device-coherently is slow). Flags live in the upper half of the
+    // counter region, 64 words per unit: a word per split and the unit's
+    // epoch (word 32). A split sets its flag to epoch + 1; the mergers wait for
+    // every flag to read epoch + 1; merger 0 then advances the epoch (every
+    // split read it before setting its flag), so nothing needs clearing and
+    // the next call in stream order waits for epoch + 2. Each split reads the
+    // epoch after its loop, once its own DMA has completed (an earlier load
+    // would shift the DMA counts the stage waits rely on). The mergers are
+    // rotated by unit % 8 so that different units' mergers, and their
+    // polling, fall on different XCDs (workgroup ids go round the XCDs, split
+    // fastest). A merger waits only for workgroups of its own unit, which on
+    // every XCD are dispatched ahead of any later unit's; its polls are
+    // bounded anyway (kFlagPollLimit).
     constexpr uint32_t RS = 16 * RB * kDecodeRecRow;                  // bytes of one split's record
     constexpr uint32_t kPairs0 = 16 * RB * 512;                       // the pairs' offset in a record
     const rsrc_t pr = make_rsrc(p.part + (int64_t) unit * p.n_split * (RS / 4), RS * (uint32_t) p.n_split);
-    unsigned * flags = p.counters + unit * kMaxSplit;
+    unsigned * flags = p.counters + kFattnCounterWords + unit * kFattnDecodeFlagWords;
+    const int K = min(p.n_split, (rows_here + p.merge_rows - 1) / p.merge_rows);
+    const int kidx = ((p.n_split - 1 - split - unit % 8) % p.n_split + p.n_split) % p.n_split;
+    unsigned epoch = 0;
     if (ws == 0) {
+        epoch = ld_agent_u32(flags + 32);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             if (rvalid[rb]) {
@@ -528,13 +534,13 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             }
         }
         complete_wave_memops();
-        if (lane == 0) st_agent_u32(flags + split, 1u);
+        if (lane == 0) st_agent_u32(flags + split, epoch + 1u);
     }
-    if (split != p.n_split - 1 - unit % min(8, p.n_split)) return;
+    if (kidx >= K) return;
     if (ws == 0) {
         for (int tries = 0;; ++tries) {
-            const unsigned f = lane < p.n_split ? ld_agent_u32(flags + lane) : 1u;
-            if (__all(f != 0u)) break;
+            const unsigned f = lane < p.n_split ? ld_agent_u32(flags + lane) : epoch + 1u;
+            if (__all(f == epoch + 1u)) break;
             if (tries >= kFlagPollLimit) {
                 if (lane == 0) atomicCAS(p.err + 2, 0, 1);
                 break;
@@ -542,22 +548,23 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             __builtin_amdgcn_s_sleep(1);
         }
         order_after_counter();
-        if (lane < p.n_split) st_agent_u32(flags + lane, 0u);         // zero again for the next call in stream order
+        if (kidx == 0 && lane == 0) st_agent_u32(flags + 32, epoch + 1u);
     }
     __syncthreads();
 
-    // The merge. The (m, l) pair of every (row, split) is loaded once
-    // (thread i takes pairs i, i + 64 WS, ...) and shared through LDS; the
-    // output items are two adjacent lanes per (row, 4 dims), each taking 16
-    // of the at most 32 splits and then combining with its partner (split
-    // half 0 first, on both lanes). A thread takes two items per round (one
-    // with two row blocks, for registers); the first round's O loads are
-    // issued before the pairs go to LDS, so a decode merge (4 rows = 256
-    // items) is one round trip.
+    // The merge of this merger's n_my rows. The (m, l) pair of every (row,
+    // split) is loaded once (thread i takes pairs i, i + 64 WS, ...) and
+    // shared through LDS; the output items are two adjacent lanes per (row,
+    // 4 dims), each taking 16 of the at most 32 splits and then combining
+    // with its partner (split half 0 first, on both lanes). The first
+    // round's O loads are issued before the pairs go to LDS, so a merger of
+    // up to 2 WS rows (WS = 2: 4 rows) makes one round trip.
+    const int n_my = (rows_here - kidx + K - 1) / K;
+    auto row_of = [&](const int lr) { return kidx + K * lr; };       // merger-local row -> row
     constexpr int kHalf = kMaxSplit / 2;
     constexpr int kItems = RB == 1 ? 2 : 1;                            // items per thread and round (registers)
     constexpr int kPairs = (16 * RB * kMaxSplit + WS * 64 - 1) / (WS * 64);
-    float2 * ml_s = (float2 *) &lds[0][0][0];                          // [row][kMaxSplit]; the rings are free
+    float2 * ml_s = (float2 *) &lds[0][0][0];                          // [local row][kMaxSplit]; the rings are free
     // (loads are unconditional, from clamped in-range addresses, and the
     // unused ones are replaced afterwards: no branch, so the O loads below
     // stay in flight while the pairs are stored)
@@ -565,10 +572,10 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 #pragma unroll
     for (int i = 0; i < kPairs; ++i) {
         const int pi = i * WS * 64 + threadIdx.x;
-        const int rr = min(pi / kMaxSplit, rows_here - 1), sp = min(pi % kMaxSplit, p.n_split - 1);
+        const int rr = row_of(min(pi / kMaxSplit, n_my - 1)), sp = min(pi % kMaxSplit, p.n_split - 1);
         mlv[i] = buf_load8_dev(pr, (uint32_t) sp * RS + kPairs0 + (uint32_t) (rr * 8));
     }
-    const int n_items = rows_here * 64;
+    const int n_items = n_my * 64;
     for (int base = 0; base < n_items; base += kItems * WS * 64) {
         float4 ov[kItems][kHalf];
 #pragma unroll
@@ -576,7 +583,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int idx = base + it2 * WS * 64 + threadIdx.x;
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
-            const int rr = idx < n_items ? idx >> 6 : 0;
+            const int rr = row_of(idx < n_items ? idx >> 6 : 0);
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
                 const int sp = min(half * kHalf + j, p.n_split - 1);
@@ -600,10 +607,10 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int idx = base + it2 * WS * 64 + threadIdx.x;
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
-            const int rr = idx < n_items ? idx >> 6 : 0;
+            const int lr = idx < n_items ? idx >> 6 : 0;
             float2 ml[kHalf];
 #pragma unroll
-            for (int j = 0; j < kHalf; ++j) ml[j] = ml_s[rr * kMaxSplit + half * kHalf + j];
+            for (int j = 0; j < kHalf; ++j) ml[j] = ml_s[lr * kMaxSplit + half * kHalf + j];
             float Mh = ml[0].x;
 #pragma unroll
             for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[j].x);
@@ -620,6 +627,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const float Lo = __shfl_xor(Lh, 1);
             const float4 ao = {__shfl_xor(ah.x, 1), __shfl_xor(ah.y, 1), __shfl_xor(ah.z, 1), __shfl_xor(ah.w, 1)};
             if (half == 0 && idx < n_items) {
+                const int rr = row_of(lr);
                 const float L = Lh + Lo;
                 const float4 acc = {ah.x + ao.x, ah.y + ao.y, ah.z + ao.z, ah.w + ao.w};
                 const int t = div_g(rr, p.G, p.g_magic);

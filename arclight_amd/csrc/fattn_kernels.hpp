@@ -36,9 +36,10 @@ struct FattnParams {
     int32_t n_split;
     int32_t cells_per_split;        // multiple of 32
     int32_t interleave;             // decode kernel: splits take every n_split-th 16-cell stage
+    int32_t merge_rows;             // decode kernel: query rows per merging workgroup
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
-    int *      err;                 // device error flags (al_device_errors): [2] prefill LDS hand-off
+    int *      err;                 // device error flags (al_device_errors): [0, 1] set_rows, [2] a merge gave up waiting
     const int32_t * dyn;            // decode kernel: device {kv_len, causal_pos0} read at run time, or null
 };
 
@@ -65,9 +66,9 @@ constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row ti
 // workgroup, `waves` wavefronts each streaming 16-cell stages of K/V through
 // a private ring of `stages` LDS buffers; fattn_decode_config_ok tells which
 // combinations exist. At most kFattnMaxSplit splits per (stream, kv head);
-// with more than one, merge records in the workspace and one flag word per
-// split in its counter region (kFattnMaxSplit words per stream x kv head);
-// the last split of each (stream, kv head) merges.
+// with more than one, merge records in the workspace and split flags in its
+// counter region (kFattnDecodeFlagWords per stream x kv head, at most
+// kFattnDecodeFlagUnits of them); min(splits, rows) splits merge.
 bool fattn_decode_config_ok(int waves, int stages);
 
 // The attention inputs of one layer folded into the decode kernel
@@ -114,4 +115,11 @@ constexpr int kFattnMaxSplit = 32;
 // per row tile or kv head), so that no call's merge records ever overlap
 // another call's counters; kernels leave it zeroed. Records follow it.
 constexpr size_t kFattnCounterBytes = 256u << 10;
-constexpr int kFattnCounterWords = (int) (kFattnCounterBytes / 4);
+// Arrival counters use the lower half of that region, which stays zero
+// between calls.
+constexpr int kFattnCounterWords = (int) (kFattnCounterBytes / 8);
+// The upper half holds the decode kernel's split flags, kFattnDecodeFlagWords
+// per (stream, kv head): a flag word per split and the unit's epoch (word
+// 32). These words carry epochs from call to call and are never cleared.
+constexpr int kFattnDecodeFlagWords = 64;
+constexpr int kFattnDecodeFlagUnits = (int) (kFattnCounterBytes / 8) / kFattnDecodeFlagWords;

@@ -94,7 +94,9 @@ typedef struct al_tensor {
  * its own buffer for the current device and args->stream (allocated on first
  * use, grown when needed; a graph captured on a stream uses that stream's).
  * A caller workspace must be zero-filled before its first use. Its first
- * 256 KiB hold arrival counters, which every call leaves at zero again;
+ * 256 KiB hold arrival counters, which every call leaves at zero again, and
+ * the decode kernel's split flags, which carry a per-(stream, kv head) epoch
+ * from call to call (zeroing the workspace again between calls is allowed);
  * per-call merge records follow them. Calls that share one workspace must
  * be ordered on one stream.
  *

@@ -208,8 +208,9 @@ def test_split_merge_repeatable_back_to_back(gpu):
 
 def test_shapes_alternating_on_one_workspace(gpu):
     # Calls of different shapes lay out their merge records differently; the
-    # arrival counters live in a fixed region no record overlaps, so
-    # alternating shapes on one workspace keeps every call correct.
+    # arrival counters and split flags live in a fixed region no record
+    # overlaps, so alternating shapes on one workspace keeps every call
+    # correct.
     from arclight_amd import device, fattn
     cases = [dict(seed=90, B=1, T=1, Hq=32, Hkv=8, n_kv=32768),
              dict(seed=91, B=2, T=2, Hq=8, Hkv=2, n_kv=2048),
@@ -235,7 +236,9 @@ def test_shapes_alternating_on_one_workspace(gpu):
             device.synchronize()
             for i, (dq, dk, dv, dst, ref) in enumerate(order):
                 assert_parity(dst.numpy(np.float32), ref, what=f"round {rnd} call {i}")
-    cnt = np.empty(65536, dtype=np.uint32)
+    # the lower half of the 256 KiB counter region holds the arrival counters
+    # (the upper half the decode split flags, which carry epochs)
+    cnt = np.empty(32768, dtype=np.uint32)
     ws.download(cnt)
     assert not cnt.any(), "arrival counters not left at zero"
 

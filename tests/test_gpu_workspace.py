@@ -146,17 +146,20 @@ def test_masked_call_replayed_with_nonprefix_then_prefix_mask(gpu):
         st.destroy()
 
 
-def test_split_flags_and_counters_left_zero(gpu):
+def test_split_flags_and_counters_across_calls(gpu):
     """Split-KV merges hand records over through the workspace's counter
-    region (the decode kernel: one flag word per split, set once the split's
-    record is stored, polled and cleared by the merging workgroup; the other
-    kernels: arrival counters). On one caller workspace, decode (4 rows),
-    4-draft verify (16 rows), 8-draft verify (32 rows, two row blocks), a
-    prefill chunk whose row tiles are split across workgroups and decode
-    again match the oracle, each twice, and the counter region reads back all
-    zeros after each."""
+    region. Its lower half holds the prefill / split-KV arrival counters,
+    which every call leaves at zero; its upper half the decode kernel's split
+    flags, 64 words per (stream, kv head): a flag per split and the unit's
+    epoch (word 32), which every multi-split decode call advances by one,
+    leaving each used flag equal to it. On one caller workspace, decode (4
+    rows), 4-draft verify (16 rows), 8-draft verify (32 rows, two row
+    blocks), a prefill chunk whose row tiles are split across workgroups and
+    decode again match the oracle, each twice, with the counter region as
+    described after each."""
     from arclight_amd import device, fattn
     region = 256 << 10
+    half = region // 8                                # words in each half
     ws = device.DeviceBuffer(region + (16 << 20))
     ws.zero()
     device.synchronize()
@@ -164,11 +167,12 @@ def test_split_flags_and_counters_left_zero(gpu):
         ("decode, 4096 cells", dict(seed=21, T=1, n_kv=4096), dict(kv_len=4000)),
         ("verify 4 drafts, 8192 cells", dict(seed=22, T=4, n_kv=8192), dict(kv_len=8196, causal_pos0=8192)),
         ("verify 8 drafts, 8192 cells", dict(seed=23, T=8, n_kv=8448), dict(kv_len=8200, causal_pos0=8192)),
-        ("256-token chunk over 512 cells (split row tiles)", dict(seed=24, T=256, n_kv=512),
-         dict(kv_len=512, causal_pos0=256)),
+        ("256-token chunk over 512 cells (split row tiles)", dict(seed=24, T=256, n_kv=2048),
+         dict(kv_len=2048, causal_pos0=1792)),
         ("decode, 1000 cells", dict(seed=25, T=1, n_kv=1024), dict(kv_len=1000)),
         ("decode, 32768 cells", dict(seed=26, T=1, n_kv=32768), dict(kv_len=32768)),
     ]
+    epoch = 0
     for name, mk, kw in cases:
         _case(name)
         q, k, v = O.make_inputs(mk["seed"], T=mk["T"], Hq=32, Hkv=8, n_kv=mk["n_kv"])
@@ -179,6 +183,11 @@ def test_split_flags_and_counters_left_zero(gpu):
         for rep in range(2):
             got = run_gpu(q, k, v, scale=SCALE, workspace=ws, **kw)
             assert_parity(got, ref, what=f"{name}, call {rep}")
-        left = ws.download(np.empty(region // 4, np.uint32))
-        nz = np.flatnonzero(left)
-        assert nz.size == 0, f"{name}: {nz.size} nonzero counter words left, first at byte {4 * nz[0]}"
+        words = ws.download(np.empty(region // 4, np.uint32))
+        nz = np.flatnonzero(words[:half])
+        assert nz.size == 0, f"{name}: {nz.size} nonzero arrival counters left, first at word {nz[0]}"
+        if mk["T"] <= 8:                              # the decode kernel, split 32 ways here
+            epoch += 2
+        flags = words[half:].reshape(-1, 64)[:8]      # the 8 kv heads of stream 0
+        assert (flags[:, 32] == epoch).all(), f"{name}: epochs {flags[:, 32]} != {epoch}"
+        assert (flags[:, 0] == epoch).all(), f"{name}: split 0 flags {flags[:, 0]} != {epoch}"
