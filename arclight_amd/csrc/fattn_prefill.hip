@@ -378,9 +378,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             mslope = SOFTCAP ? slope : slope / p.scale;
         }
         // Q^T B operands: row rr (token r / G, head kvh G + r % G), dims
-        // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers
+        // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers; the
+        // loads go out before barrier (Q), their latency overlapping the
+        // producers' first DMA
         half8 qf[8];
-        __syncthreads();                          // (Q) the first K/V tiles are on their way
         {
             const int r = row0 + (rvalid ? rr : 0);
             const int tk = tok_of(r);
@@ -392,6 +393,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 qv[2 * ks] = *(const float4 *) (qrow + 16 * ks + 8 * h);
                 qv[2 * ks + 1] = *(const float4 *) (qrow + 16 * ks + 8 * h + 4);
             }
+            __syncthreads();                          // (Q) the first K/V tiles are on their way
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks)
                 qf[ks] = rvalid ? to_half8(qv[2 * ks], qv[2 * ks + 1]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
