@@ -381,24 +381,42 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // 16 ks + 8 h .. + 7, f16 (RNE), loaded straight into registers; the
         // loads go out before barrier (Q), their latency overlapping the
         // producers' first DMA
+        // With two cell splits the rows of a row group are loaded once, by
+        // split 0's wave, and handed to split 1's as f16 through split 1's V
+        // buffer 2 (16 KiB for 64 rows; its first DMA goes out after barrier
+        // B_0): every CU reads its query rows once.
         half8 qf[8];
+        constexpr bool kShareQ = S::SP == 2;
+        char * const qshare = lds + S::RING + NK * kTileBytes + 2 * kTileBytes;   // split 1's V buffer 2
+        static_assert(!kShareQ || NV >= 3, "the shared query rows need a V buffer the prologue leaves free");
+        auto qslot = [&](const int ks) { return rr * 256 + ((((2 * ks + h) ^ (rr & 15)) & 15) << 4); };
         {
             const int r = row0 + (rvalid ? rr : 0);
             const int tk = tok_of(r);
             const float * qrow = (const float *) (p.q + (int64_t) b * p.q_nb3 + (int64_t) tk * p.q_nb1 +
                                                   (int64_t) (kvh * p.G + r - tk * p.G) * p.q_nb2);
             float4 qv[16];
+            if (!kShareQ || si == 0) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                qv[2 * ks] = *(const float4 *) (qrow + 16 * ks + 8 * h);
-                qv[2 * ks + 1] = *(const float4 *) (qrow + 16 * ks + 8 * h + 4);
+                for (int ks = 0; ks < 8; ++ks) {
+                    qv[2 * ks] = *(const float4 *) (qrow + 16 * ks + 8 * h);
+                    qv[2 * ks + 1] = *(const float4 *) (qrow + 16 * ks + 8 * h + 4);
+                }
             }
             __syncthreads();                          // (Q) the first K/V tiles are on their way
+            if (!kShareQ || si == 0) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-                qf[ks] = rvalid ? to_half8(qv[2 * ks], qv[2 * ks + 1]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+                for (int ks = 0; ks < 8; ++ks) {
+                    qf[ks] = rvalid ? to_half8(qv[2 * ks], qv[2 * ks + 1]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
+                    if (kShareQ) *(half8 *) (qshare + qslot(ks)) = qf[ks];
+                }
+            }
         }
         __syncthreads();                          // (1)
+        if (kShareQ && si == 1) {
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) qf[ks] = *(const half8 *) (qshare + qslot(ks));
+        }
 
         // LDS read offsets of this lane: K operand (cell 32 cb + lr, granule
         // 2 ks + h) and V^T operand (cell 16 kk + 4 h + (s16 >> 2) [+ 8],
