@@ -74,6 +74,16 @@ __device__ __forceinline__ void st_agent_u32(unsigned * p, unsigned v) {
 __device__ __forceinline__ unsigned ld_agent_u32(const unsigned * p) {
     return __hip_atomic_load(const_cast<unsigned *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A wave-uniform read of memory that no kernel running alongside writes,
+// as a scalar load (lgkm-counted): through the constant address space, so
+// that it is scalar whatever else the kernel does to memory (an asm
+// statement with side effects before it keeps the compiler from proving
+// that for a global pointer, and it would then issue a vector load).
+template <typename T>
+__device__ __forceinline__ T ld_uniform(const T * ptr) {
+    return *(const __attribute__((address_space(4))) T *) ptr;
+}
+
 // Polls of a merging workgroup for the split flags of its launch before it
 // gives up and reports it (each poll a round trip to the coherence point
 // after a short sleep: about a second in all).

@@ -38,11 +38,12 @@
 // lie past the run-time length publish empty records.
 //
 // Merge. The WS waves merge their online-softmax states through LDS. With
-// one split the workgroup then writes dst; otherwise it publishes one
-// record per row with device-coherent stores, bumps the arrival counter of
-// its (stream, kv head), and the last workgroup to arrive merges the at most
-// 32 splits (all loads in flight, fixed order, so results are
-// bit-reproducible) and writes dst.
+// one split the workgroup then writes dst; otherwise it publishes its
+// record with device-coherent stores and then its split flag, and
+// min(splits, rows / merge_rows) of the (stream, kv head)'s workgroups wait
+// for every flag and merge the at most 32 splits of their share of the rows
+// (all loads in flight, fixed order, so results are bit-reproducible) into
+// dst.
 
 #include "fattn_tile.hpp"
 
@@ -66,10 +67,13 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
     __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
-    // fused inputs: 1 KiB slots of q_w, k_w, the new token's k and v rows
-    // for this kv head (512 bytes each), its position and its cache row
-    constexpr int kPieces = 6;
-    __shared__ __attribute__((aligned(1024))) char fin[FUSED ? kPieces * 1024 : 16];
+    // fused inputs: 1 KiB slots of q_w, k_w and the new token's k and v rows
+    // for this kv head (512 bytes each), then the new K (normed, rotated) and
+    // V rows as f16 (256 bytes each) and the rotation pairs' (cos, sin)
+    constexpr int kPieces = 4;
+    __shared__ __attribute__((aligned(1024))) char fin[FUSED ? kPieces * 1024 + 1024 : 16];
+    char * const kv16 = fin + kPieces * 1024;
+    float2 * const rot_tab = (float2 *) (fin + kPieces * 1024 + 512);
     prefetch_params(p);
 
     const int lane = threadIdx.x & 63;
@@ -86,23 +90,26 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const int rows_here = min(16 * RB, p.R);
     const int t_last = div_g(rows_here - 1, p.G, p.g_magic);
 
-    // lengths: fixed at launch, or read now (a graph replayed per decode step)
-    int hi = p.kv_hi;
-    int64_t cpos0 = p.causal_pos0;
-    if (p.dyn) {
-        hi = min(max(p.dyn[0], 0), p.kv_hi);
-        if (cpos0 >= 0) cpos0 = max(p.dyn[1], 0);
-    }
-    if (cpos0 >= 0) hi = (int) min((int64_t) hi, cpos0 + t_last + 1);
+    // Lengths: fixed at launch, or (p.dyn: a graph replayed per decode step)
+    // read when the kernel runs, within the launch's kv_len. The first
+    // stages are issued against the launch's bound while the run-time
+    // length is on its way (scalar loads): a stage past the run-time length
+    // is then loaded and not used, and the buffer ranges keep every load
+    // inside the cache.
+    auto limit = [&](const int h, const int64_t c0) { return c0 >= 0 ? (int) min((int64_t) h, c0 + t_last + 1) : h; };
     // Stages of this workgroup: with interleave, global 16-cell stages
     // split, split + n_split, ... of [0, hi) (all splits of a head sweep the
     // cache together); else the contiguous range [c_begin, c_end). Wave ws
     // takes the workgroup's stages ws, ws + WS, ...
     const int c_begin = p.interleave ? 16 * split : split * p.cells_per_split;
-    const int c_end = p.interleave ? hi : min(c_begin + p.cells_per_split, hi);
     const int sstride = p.interleave ? kSC * p.n_split : kSC;              // cells between the workgroup's stages
-    const int ns = c_end > c_begin ? (c_end - c_begin + sstride - 1) / sstride : 0;
-    const int my_ns = ns > ws ? (ns - ws + WS - 1) / WS : 0;
+    auto range_end = [&](const int h) { return p.interleave ? h : min(c_begin + p.cells_per_split, h); };
+    auto wave_stages = [&](const int h) {
+        const int c_e = range_end(h);
+        const int ns = c_e > c_begin ? (c_e - c_begin + sstride - 1) / sstride : 0;
+        return ns > ws ? (ns - ws + WS - 1) / WS : 0;
+    };
+    const int n_pre = min(NB - 1, wave_stages(p.dyn ? p.kv_hi : limit(p.kv_hi, p.causal_pos0)));  // issued ahead
 
     // K/V rows of this stream and head (loads past the end read 0)
     const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
@@ -179,8 +186,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             dma16(qd, qofs + ((qslot ^ (uint32_t) (2 * (r2 & 15))) & 31) * 16, lds_addr(qlds) + (uint32_t) (i * 1024));
         }
     }
-    // fused: the weights, this kv head's new K / V rows, the position and
-    // the cache row travel the same way (piece i by wave i % WS)
+    // fused: the weights and this kv head's new K / V rows travel the same
+    // way (piece i by wave i % WS)
     if constexpr (FUSED) {
         for (int i = ws; i < kPieces; i += WS) {
             const char * src;
@@ -188,62 +195,151 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             if (i == 0) src = in.q_w;
             else if (i == 1) src = in.k_w;
             else if (i == 2) src = in.k + kvh * in.k_nb1;
-            else if (i == 3) src = in.v + kvh * 512;
-            else if (i == 4) { src = (const char *) in.pos; bytes = 4; }
-            else { src = in.rows; bytes = (uint32_t) in.rows_nb0; }
-            if (src) dma16(raw_desc(src, bytes), (uint32_t) lane * 16, lds_addr(fin) + (uint32_t) (i * 1024));
+            else src = in.v + kvh * 512;
+            if (src) dma16(raw_desc(src, 512), (uint32_t) lane * 16, lds_addr(fin) + (uint32_t) (i * 1024));
         }
+    }
+    // Scalar loads (lgkm-counted, so the DMA waits are unaffected), issued
+    // after the query rows' DMA and before the stages' (measured faster than
+    // after them, where they queue behind the stages' traffic): the run-time
+    // length (unconditional, from the error flags when there is no p.dyn, as
+    // a branch would wait for them at once) and, fused, the token's position
+    // and cache row (both words of an i64 row, or the i32 row twice).
+    const int32_t * dsrc = p.dyn ? p.dyn : p.err;
+    const int32_t dyn_len = ld_uniform(dsrc), dyn_pos0 = ld_uniform(dsrc + 1);
+    int32_t pos_0 = 0;
+    int64_t row_0 = 0;
+    if constexpr (FUSED) {
+        pos_0 = ld_uniform(in.pos);
+        const uint32_t * rw = (const uint32_t *) in.rows;
+        const uint32_t rlo = ld_uniform(rw), rhi = ld_uniform(rw + (in.rows64 ? 1 : 0));
+        row_0 = in.rows64 ? (int64_t) (((uint64_t) rhi << 32) | rlo) : (int64_t) (int32_t) rlo;
     }
 #pragma unroll
     for (int u = 0; u < NB - 1; ++u)
-        if (u < my_ns) issue(u, u);
+        if (u < n_pre) issue(u, u);
+    // fused: wave 0 tabulates the rotation pairs' (cos, sin), lane i pair i
+    // (while the DMA is in flight; the barrier below publishes it)
+    if constexpr (FUSED) {
+        if (ws == 0) {
+            float c, sn;
+            rope_cos_sin<FM>(in.rope, pos_0, lane, c, sn);
+            rot_tab[lane] = float2{c, sn};
+        }
+    }
+
+    // the run-time length (at most the launch's bound, so my_ns <= the
+    // stages issued ahead + whatever the loop issues)
+    int hi = p.kv_hi;
+    int64_t cpos0 = p.causal_pos0;
+    if (p.dyn) {
+        hi = min(max(dyn_len, 0), p.kv_hi);
+        if (cpos0 >= 0) cpos0 = max(dyn_pos0, 0);
+    }
+    hi = limit(hi, cpos0);
+    const int c_end = range_end(hi);
+    const int my_ns = wave_stages(hi);
+
     // own query rows landed (the stages were issued after them), then everyone's
-    wait_later<NB - 1, PER>(min(NB - 1, my_ns));
+    wait_later<NB - 1, PER>(n_pre);
     __syncthreads();
 
-    // fused: this wave's query rows through RMSNorm, weight and rotation in
-    // place; the new tokens' K (normed, rotated) and V rows of this kv head,
-    // f16, for the wave whose stage holds the token's cell (it patches the
-    // stage) and for split 0's wave 0 (it writes the cache)
+    // fused: the query rows through RMSNorm, weight and rotation in place,
+    // and the new token's K row (normed, rotated) and V row as f16 (kv16),
+    // for the wave whose stage holds the token's cell (it patches the stage)
+    // and for split 0 (it writes the cache). Rows go to slots of 8 lanes:
+    // slot s = 8 ws + lane / 8 (+ 8 WS per further pass) takes query row s
+    // below rows_here and the K row at rows_here; lane t = lane % 8 of a slot
+    // holds rotation pairs 8t..8t+7 (NEOX: dims 8t + k and 64 + 8t + k; pairs
+    // (2i, 2i + 1) and no rotation: dims 16t + 2k and 16t + 2k + 1). Every
+    // lane of a wave with a live slot computes (the row sums are shuffles);
+    // only live slots store.
     int cell_0 = -1;                                                   // the new cell, -1 if out of range
     int j_own = -1;                                                    // this wave's stage that holds it
-    int64_t row_0 = 0;
-    half2v kvk = {0, 0}, kvv = {0, 0};
     if constexpr (FUSED) {
-        const int d0 = rope_d0<FM>(lane), d1 = rope_d1<FM>(lane);
-        const int32_t pos_0 = __builtin_amdgcn_readfirstlane(*(const int32_t *) (fin + 4 * 1024));
-        const uint32_t rlo = __builtin_amdgcn_readfirstlane(*(const uint32_t *) (fin + 5 * 1024));
-        const uint32_t rhi = __builtin_amdgcn_readfirstlane(*(const uint32_t *) (fin + 5 * 1024 + 4));
-        row_0 = in.rows64 ? (int64_t) (((uint64_t) rhi << 32) | rlo) : (int64_t) (int32_t) rlo;
-        float cos_0, sin_0;
-        rope_cos_sin<FM>(in.rope, pos_0, lane, cos_0, sin_0);
-        const float * qw = (const float *) fin;
-        const float * kw = (const float *) (fin + 1024);
+        const int t = lane & 7;
+        float2 rot[8];
+#pragma unroll
+        for (int k = 0; k < 8; k += 2) {
+            const float4 x = *(const float4 *) (rot_tab + 8 * t + k);
+            rot[k] = float2{x.x, x.y};
+            rot[k + 1] = float2{x.z, x.w};
+        }
         const bool has_qw = in.q_w != nullptr, has_kw = in.k_w != nullptr;
-        const float qw0 = has_qw ? qw[d0] : 1.0f, qw1 = has_qw ? qw[d1] : 1.0f;
-        for (int r = ws; r < rows_here; r += WS) {
-            char * row = qlds + r * 512;
-            float * x0p = (float *) (row + (((d0 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d0 & 3) * 4);
-            float * x1p = (float *) (row + (((d1 >> 2) ^ (2 * (r & 15))) & 31) * 16 + (d1 & 3) * 4);
-            float y0, y1;
-            norm_rope_apply<FM>(*x0p, *x1p, has_qw, qw0, qw1, in.eps, cos_0, sin_0, y0, y1);
-            *x0p = y0;
-            *x1p = y1;
+        // the lane's four granules (4 dims each) of a row
+        int gi[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) gi[m] = FM == 2 ? (m < 2 ? 2 * t + m : 16 + 2 * t + m - 2) : 4 * t + m;
+        const int passes = (rows_here + 8 * WS) / (8 * WS);
+        for (int pass = 0; pass < passes; ++pass) {
+            const int s0 = pass * 8 * WS + 8 * ws;                       // the wave's first slot
+            if (s0 > rows_here) continue;
+            const int sl = s0 + (lane >> 3);
+            const bool is_q = sl < rows_here, is_k = sl == rows_here;
+            const int r = is_q ? sl : 0;
+            const bool has_w = is_k ? has_kw : has_qw;
+            const char * wsrc = fin + (is_k ? 1024 : 0);
+            char * src[4];
+            float4 a[4], w[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                // granule j of query row r sits at slot (j ^ 2(r & 15)) & 31
+                src[m] = is_k ? fin + 2 * 1024 + gi[m] * 16 : qlds + r * 512 + (((gi[m] ^ (2 * (r & 15))) & 31) << 4);
+                a[m] = *(const float4 *) src[m];
+                w[m] = has_w ? *(const float4 *) (wsrc + gi[m] * 16) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+            }
+            float lo[8], hi[8], wl[8], wh[8], ylo[8], yhi[8];
+            if constexpr (FM == 2) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    lo[4 * m] = a[m].x; lo[4 * m + 1] = a[m].y; lo[4 * m + 2] = a[m].z; lo[4 * m + 3] = a[m].w;
+                    hi[4 * m] = a[m + 2].x; hi[4 * m + 1] = a[m + 2].y; hi[4 * m + 2] = a[m + 2].z; hi[4 * m + 3] = a[m + 2].w;
+                    wl[4 * m] = w[m].x; wl[4 * m + 1] = w[m].y; wl[4 * m + 2] = w[m].z; wl[4 * m + 3] = w[m].w;
+                    wh[4 * m] = w[m + 2].x; wh[4 * m + 1] = w[m + 2].y; wh[4 * m + 2] = w[m + 2].z; wh[4 * m + 3] = w[m + 2].w;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    lo[2 * m] = a[m].x; hi[2 * m] = a[m].y; lo[2 * m + 1] = a[m].z; hi[2 * m + 1] = a[m].w;
+                    wl[2 * m] = w[m].x; wh[2 * m] = w[m].y; wl[2 * m + 1] = w[m].z; wh[2 * m + 1] = w[m].w;
+                }
+            }
+            norm_rope_group8<FM>(lo, hi, wl, wh, in.eps, rot, ylo, yhi);
+            float4 y[4];
+            if constexpr (FM == 2) {
+#pragma unroll
+                for (int m = 0; m < 2; ++m) {
+                    y[m] = float4{ylo[4 * m], ylo[4 * m + 1], ylo[4 * m + 2], ylo[4 * m + 3]};
+                    y[m + 2] = float4{yhi[4 * m], yhi[4 * m + 1], yhi[4 * m + 2], yhi[4 * m + 3]};
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) y[m] = float4{ylo[2 * m], yhi[2 * m], ylo[2 * m + 1], yhi[2 * m + 1]};
+            }
+            if (is_q) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) *(float4 *) src[m] = y[m];
+            }
+            if (is_k) {
+                // granule gi of the K row is dims 4gi..4gi+3: f16 at kv16 + 8gi;
+                // the V row's dims 16t..16t+15 likewise at kv16 + 256 + 32t
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    *(half4 *) (kv16 + gi[m] * 8) =
+                        half4{(_Float16) y[m].x, (_Float16) y[m].y, (_Float16) y[m].z, (_Float16) y[m].w};
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float4 v = *(const float4 *) (fin + 3 * 1024 + (4 * t + m) * 16);
+                    *(half4 *) (kv16 + 256 + (4 * t + m) * 8) =
+                        half4{(_Float16) v.x, (_Float16) v.y, (_Float16) v.z, (_Float16) v.w};
+                }
+            }
         }
         cell_0 = row_0 >= 0 && row_0 < in.n_rows ? (int) row_0 : -1;
         const int rel = cell_0 - c_begin;
         if (cell_0 >= 0 && rel >= 0 && cell_0 < c_end && rel % sstride < kSC && (rel / sstride) % WS == ws)
             j_own = (rel / sstride) / WS;
-        if (j_own >= 0 || (split == 0 && ws == 0)) {
-            const float kw0 = has_kw ? kw[d0] : 1.0f, kw1 = has_kw ? kw[d1] : 1.0f;
-            const float * kr = (const float *) (fin + 2 * 1024);
-            const float * vr = (const float *) (fin + 3 * 1024);
-            float y0, y1;
-            norm_rope_apply<FM>(kr[d0], kr[d1], has_kw, kw0, kw1, in.eps, cos_0, sin_0, y0, y1);
-            kvk = half2v{(_Float16) y0, (_Float16) y1};
-            kvv = half2v{(_Float16) vr[d0], (_Float16) vr[d1]};
-        }
-        __syncthreads();                                               // every query row ready
+        __syncthreads();                                               // every query row and kv16 ready
     }
 
     // Q^T B-operand fragments: k slots of block kb, group g = dims 32kb + 8g..+8
@@ -303,15 +399,12 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int cs = c_begin + sstride * (ws + j * WS);
             if constexpr (FUSED) {
                 // the new token's rows replace the cache's copy of its cell
-                // (granule j of cell c at slot j ^ c)
-                if (j == j_own) {
+                // (granule j of cell c at slot j ^ c): lanes 0..15 K, 16..31 V
+                if (j == j_own && lane < 32) {
                     const int c = cell_0 - cs;
-                    const int d0 = rope_d0<FM>(lane), d1 = rope_d1<FM>(lane);
-                    char * sw = &lds[ws][u][0] + c * 256;
-                    *(_Float16 *) (sw + (((d0 >> 3) ^ c) << 4) + (d0 & 7) * 2) = kvk[0];
-                    *(_Float16 *) (sw + (((d1 >> 3) ^ c) << 4) + (d1 & 7) * 2) = kvk[1];
-                    *(_Float16 *) (sw + 4096 + (((d0 >> 3) ^ c) << 4) + (d0 & 7) * 2) = kvv[0];
-                    *(_Float16 *) (sw + 4096 + (((d1 >> 3) ^ c) << 4) + (d1 & 7) * 2) = kvv[1];
+                    const int gj = lane & 15, part = lane >> 4;
+                    *(u32x4 *) (&lds[ws][u][0] + part * 4096 + c * 256 + ((gj ^ c) << 4)) =
+                        *(const u32x4 *) (kv16 + part * 256 + gj * 16);
                 }
             }
             u32x4 kf[4];
@@ -402,6 +495,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                 for (int mb = 0; mb < 8; ++mb) o[rb][mb] = mfma_16x16x16(vt[mb], pf[rb], o[rb][mb]);
         }
     }
+    // stages issued ahead and not used (my_ns == 0 at run time) land before
+    // the rings are reused (with my_ns > 0 the loop's last wait took them)
+    wait_later<NB - 1, PER>(0);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) l_run[rb] = colsum4(l_run[rb]);
 
@@ -427,10 +523,12 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                 } else {
                     _Float16 * kc = (_Float16 *) (in.k_cache + (int64_t) cell_0 * in.kc_nb1) + kvh * 128;
                     _Float16 * vc = (_Float16 *) (in.v_cache + (int64_t) cell_0 * in.vc_nb1) + kvh * 128;
-                    kc[d0] = kvk[0];
-                    kc[d1] = kvk[1];
-                    vc[d0] = kvv[0];
-                    vc[d1] = kvv[1];
+                    const _Float16 * k16 = (const _Float16 *) kv16;
+                    const _Float16 * v16 = (const _Float16 *) (kv16 + 256);
+                    kc[lane] = k16[lane];
+                    kc[lane + 64] = k16[lane + 64];
+                    vc[lane] = v16[lane];
+                    vc[lane + 64] = v16[lane + 64];
                 }
             }
         }

@@ -474,38 +474,32 @@ __device__ __forceinline__ uint32_t lds_addr(const void * p) {
     return (uint32_t) (uintptr_t) (const __attribute__((address_space(3))) char *) p;
 }
 
-// Waits until at most `later` stages of PER memory operations each are still
-// outstanding (the stages issued after the one about to be read).
-template <int NB, int PER>
-__device__ __forceinline__ void wait_stage(int later) {
-    mem_barrier();
-    if constexpr (NB >= 4) {
-        if (later >= 2) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); mem_barrier(); return; }
+template <int K, int PER>
+__device__ __forceinline__ void wait_vm_stages(int k) {
+    if constexpr (K > 0) {
+        if (k >= K) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(K * PER)); return; }
+        wait_vm_stages<K - 1, PER>(k);
+    } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
     }
-    if constexpr (NB >= 3) {
-        if (later >= 1) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); mem_barrier(); return; }
-    }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-    mem_barrier();
 }
 
 // Waits until at most k * PER memory operations are outstanding (0 <= k <=
-// KMAX <= 3): the k stages issued after the data about to be read.
+// KMAX): the k stages issued after the data about to be read.
 template <int KMAX, int PER>
 __device__ __forceinline__ void wait_later(int k) {
-    static_assert(KMAX <= 3 && 3 * PER < 64, "vmcnt holds at most 63");
+    static_assert(KMAX >= 0 && KMAX * PER < 64, "vmcnt holds at most 63");
     mem_barrier();
-    if constexpr (KMAX >= 3) {
-        if (k >= 3) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(3 * PER)); mem_barrier(); return; }
-    }
-    if constexpr (KMAX >= 2) {
-        if (k >= 2) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PER)); mem_barrier(); return; }
-    }
-    if constexpr (KMAX >= 1) {
-        if (k >= 1) { __builtin_amdgcn_s_waitcnt(vmcnt_imm(PER)); mem_barrier(); return; }
-    }
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    wait_vm_stages<KMAX, PER>(k);
     mem_barrier();
+}
+
+// Waits until at most `later` (<= NB - 2) stages of PER memory operations
+// each are still outstanding (the stages issued after the one about to be
+// read, in a ring of NB).
+template <int NB, int PER>
+__device__ __forceinline__ void wait_stage(int later) {
+    wait_later<NB - 2, PER>(later);
 }
 
 }  // namespace fattn

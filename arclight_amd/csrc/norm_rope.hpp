@@ -81,6 +81,48 @@ __device__ __forceinline__ void norm_rope_apply(const float x0, const float x1, 
     }
 }
 
+// RMSNorm, weight and rotation of rows held by groups of 8 lanes (lanes
+// 8i..8i+7 of a wave hold one row), each lane with 8 rotation pairs: lo[k]
+// and hi[k] are the two dims of the lane's pair k, w_lo / w_hi their
+// weights (1 where there is no weight, which leaves the product bit for bit
+// unchanged), rot[k] the pair's (cos, sin). Per value the arithmetic of
+// norm_rope_apply; the row's sum of squares (double) is added in another
+// order, so the two can differ only where the partial sums are not exact in
+// double, by rounding in the double's last bits, far below the f32 mean's
+// resolution. Every lane of the wave takes part (the sum's shuffles).
+template <int MODE>
+__device__ __forceinline__ void norm_rope_group8(const float (&lo)[8], const float (&hi)[8], const float (&w_lo)[8],
+                                                 const float (&w_hi)[8], const float eps, const float2 (&rot)[8],
+                                                 float (&y_lo)[8], float (&y_hi)[8]) {
+#pragma clang fp contract(off)
+    double part[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float a = lo[k] * lo[k], b = hi[k] * hi[k];
+        part[k] = (double) a + (double) b;
+    }
+#pragma unroll
+    for (int h = 4; h >= 1; h /= 2)
+#pragma unroll
+        for (int k = 0; k < h; ++k) part[k] += part[k + h];
+    double sum = part[0];
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 4);
+    const float mean = (float) (sum / 128.0);
+    const float scale = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float n0 = (lo[k] * scale) * w_lo[k], n1 = (hi[k] * scale) * w_hi[k];
+        y_lo[k] = n0;
+        y_hi[k] = n1;
+        if constexpr (MODE != 0) {
+            y_lo[k] = n0 * rot[k].x - n1 * rot[k].y;
+            y_hi[k] = n0 * rot[k].y + n1 * rot[k].x;
+        }
+    }
+}
+
 // Both steps for one row.
 template <int MODE>
 __device__ __forceinline__ void norm_rope_pair(const float x0, const float x1, const bool has_w, const float w0,
