@@ -97,17 +97,20 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     // is then loaded and not used, and the buffer ranges keep every load
     // inside the cache.
     auto limit = [&](const int h, const int64_t c0) { return c0 >= 0 ? (int) min((int64_t) h, c0 + t_last + 1) : h; };
-    // Stages of this workgroup: with interleave, global 16-cell stages
-    // split, split + n_split, ... of [0, hi) (all splits of a head sweep the
-    // cache together); else the contiguous range [c_begin, c_end). Wave ws
-    // takes the workgroup's stages ws, ws + WS, ...
-    const int c_begin = p.interleave ? 16 * split : split * p.cells_per_split;
-    const int sstride = p.interleave ? kSC * p.n_split : kSC;              // cells between the workgroup's stages
+    // Stages of this wave: cells wbase + wstride j .. + 15 below the range's
+    // end. With interleave the workgroup takes global 16-cell stages split,
+    // split + n_split, ... of [0, hi) and wave ws every WS-th of them, so all
+    // splits of a head sweep the cache together (measured faster than
+    // contiguous ranges, and than blocks of WS adjacent stages, one per
+    // wave); else the workgroup's contiguous range [c_begin, c_begin +
+    // cells_per_split), wave ws taking its stages ws, ws + WS, ...
+    const int c_begin = p.interleave ? 0 : split * p.cells_per_split;
+    const int wbase = p.interleave ? kSC * (split + p.n_split * ws) : c_begin + kSC * ws;
+    const int wstride = p.interleave ? kSC * WS * p.n_split : kSC * WS;
     auto range_end = [&](const int h) { return p.interleave ? h : min(c_begin + p.cells_per_split, h); };
     auto wave_stages = [&](const int h) {
         const int c_e = range_end(h);
-        const int ns = c_e > c_begin ? (c_e - c_begin + sstride - 1) / sstride : 0;
-        return ns > ws ? (ns - ws + WS - 1) / WS : 0;
+        return c_e > wbase ? (c_e - wbase + wstride - 1) / wstride : 0;
     };
     const int n_pre = min(NB - 1, wave_stages(p.dyn ? p.kv_hi : limit(p.kv_hi, p.causal_pos0)));  // issued ahead
 
@@ -157,9 +160,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         msrc = (uint32_t) ((int64_t) mt_ * p.m_nb1 + (int64_t) (mh % p.m_ne2) * p.m_nb2) + (uint32_t) ((lane & 1) * 16);
     }
 
-    // This wave's j-th stage (cells c_begin + sstride (ws + j WS) ..) into ring slot u.
+    // This wave's j-th stage (cells wbase + wstride j ..) into ring slot u.
     auto issue = [&](const int j, const int u) {
-        const uint32_t cs = (uint32_t) (c_begin + sstride * (ws + j * WS));
+        const uint32_t cs = (uint32_t) (wbase + wstride * j);
         const uint32_t kofs = cs * k_nb1 + dk, vofs = cs * v_nb1 + dv;
         const uint32_t base = ring + (uint32_t) (u * STAGE);
 #pragma unroll
@@ -336,9 +339,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             }
         }
         cell_0 = row_0 >= 0 && row_0 < in.n_rows ? (int) row_0 : -1;
-        const int rel = cell_0 - c_begin;
-        if (cell_0 >= 0 && rel >= 0 && cell_0 < c_end && rel % sstride < kSC && (rel / sstride) % WS == ws)
-            j_own = (rel / sstride) / WS;
+        const int rel = cell_0 - wbase;
+        if (cell_0 >= 0 && rel >= 0 && cell_0 < c_end && rel % wstride < kSC) j_own = rel / wstride;
         __syncthreads();                                               // every query row and kv16 ready
     }
 
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             if (j + NB - 1 < my_ns) issue(j + NB - 1, (u + NB - 1) % NB);
             mem_barrier();
             const char * st = &lds[ws][u][0];
-            const int cs = c_begin + sstride * (ws + j * WS);
+            const int cs = wbase + wstride * j;
             if constexpr (FUSED) {
                 // the new token's rows replace the cache's copy of its cell
                 // (granule j of cell c at slot j ^ c): lanes 0..15 K, 16..31 V
