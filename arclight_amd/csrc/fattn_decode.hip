@@ -684,6 +684,13 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
             const int rr = row_of(idx < n_items ? idx >> 6 : 0);
+            // an item slot of a round past the merger's items loads nothing
+            // (a uniform branch: 8 waves with 8 rows fill one slot per thread)
+            if (it2 > 0 && base + it2 * WS * 64 >= n_items) {
+#pragma unroll
+                for (int j = 0; j < kHalf; ++j) ov[it2][j] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+                continue;
+            }
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
                 const int sp = min(half * kHalf + j, p.n_split - 1);
