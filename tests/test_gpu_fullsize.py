@@ -76,6 +76,27 @@ def test_prefill_qwen3_32b_chunk1024(gpu, pos0):
     assert_parity(got[:, sel], ref, what=f"prefill 32B chunk pos0 {pos0} ({len(sel)} tokens)")
 
 
+def test_prefill_qwen3_32b_explicit_mask_then_split_decode(gpu):
+    # the 32B 1024-token chunk as nnml calls it (the f16 mask tensor, no
+    # length hints), then a split decode on the same library workspace: the
+    # masked call must leave the workspace's arrival counters and split
+    # flags as the decode expects them
+    T, pos0 = 1024, 1024
+    kv_len = pos0 + T
+    q, k, v = O.make_inputs(7001, T=T, Hq=64, Hkv=8, n_kv=kv_len)
+    m = O.causal_mask(T, kv_len, pos0, kv_len=kv_len)
+    _case("prefill Qwen3-32B shape chunk 1024 pos0 1024, explicit mask")
+    got = run_gpu(q, k, v, m, scale=SCALE)
+    rng = np.random.default_rng(7)
+    sel = np.unique(np.concatenate([[0, 1, 63, 64, T - 1], rng.choice(T, 27, replace=False)]))
+    assert_parity(got[:, sel], _sampled_ref(q, k, v, sel, pos0, kv_len), what="prefill 32B explicit mask")
+    qd, kd, vd = O.make_inputs(7002, T=1, Hq=32, Hkv=8, n_kv=16384)
+    _case("decode ctx 16384 after the masked prefill")
+    for rep in range(2):
+        assert_parity(run_gpu(qd, kd, vd, scale=SCALE, kv_len=16384), O.attention(qd, kd, vd, scale=SCALE, kv_len=16384),
+                      what=f"split decode after masked prefill, call {rep}")
+
+
 def test_prefill_chunks_equal_one_causal_call(gpu):
     # 2048-token Qwen3-4B-shape prompt: 4 chunks of 512 (chunk c sees cells
     # [0, 512 (c + 1))) against one causal call over all 2048 tokens
