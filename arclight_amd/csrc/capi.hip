@@ -616,8 +616,8 @@ extern "C" int al_fattn_f16_worker(const al_fattn_args * a, int ith, int nth) {
 // no-allocation entry point
 // ---------------------------------------------------------------------------
 
-// The scratch of al_fattn_f16_noalloc: arrival counters and merge records,
-// laid out as a caller workspace. One copy per GPU,
+// The scratch of al_fattn_f16_noalloc: arrival counters, decode split flags
+// and merge records, laid out as a caller workspace. One copy per GPU,
 // held until the process ends; every call on that GPU shares it.
 static __device__ __align__(256) unsigned char scratch[AL_FATTN_NOALLOC_SCRATCH_BYTES];
 

@@ -161,7 +161,8 @@ uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Same
  * validation, kernels and results as al_fattn_f16; args->workspace is
- * ignored. The scratch (arrival counters and merge records) is a file-scope
+ * ignored. The scratch (arrival counters, decode split flags and merge
+ * records) is a file-scope
  * device array of
  * AL_FATTN_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends. A
  * call that needs more (al_fattn_workspace_bytes) fails with
