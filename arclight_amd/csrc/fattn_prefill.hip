@@ -180,11 +180,23 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 for (int q = 0; q < 8; ++q) {
                     const int j = j0 + 64 * q + lane;
                     if (j >= n8) continue;
+                    // 8 cells at once when they are all +-0 or all -inf (the
+                    // two values a causal mask holds), else value by value
                     const uint32_t x[4] = {w[q].x, w[q].y, w[q].z, w[q].w};
+                    const bool zeros = ((x[0] | x[1] | x[2] | x[3]) & 0x7fff7fffu) == 0u;
+                    const bool infs = x[0] == 0xfc00fc00u && x[1] == 0xfc00fc00u && x[2] == 0xfc00fc00u &&
+                                      x[3] == 0xfc00fc00u;
+                    if (zeros) {
+                        last_fin = max(last_fin, 8 * j + 7);
+                        last0 = max(last0, 8 * j + 7);
+                    } else if (infs) {
+                        first_inf = min(first_inf, 8 * j);
+                    } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        classify(x[e] & 0xffffu, 8 * j + 2 * e);
-                        classify(x[e] >> 16, 8 * j + 2 * e + 1);
+                        for (int e = 0; e < 4; ++e) {
+                            classify(x[e] & 0xffffu, 8 * j + 2 * e);
+                            classify(x[e] >> 16, 8 * j + 2 * e + 1);
+                        }
                     }
                 }
             }
