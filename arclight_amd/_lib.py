@@ -19,6 +19,8 @@ SIGNATURES = {
     "al_fattn_f16": (_I, [ctypes.POINTER(abi.AlFattnArgs)]),
     "al_fattn_workspace_bytes": (_U64, [ctypes.POINTER(abi.AlFattnArgs)]),
     "al_fattn_f16_worker": (_I, [ctypes.POINTER(abi.AlFattnArgs), _I, _I]),
+    "al_fattn_apply_node_hints": (_I, [ctypes.POINTER(abi.AlFattnArgs), ctypes.POINTER(ctypes.c_int32)]),
+    "al_fattn_release_stream": (_I, [_VP]),
     "al_fattn_noalloc_init": (_I, []),
     "al_fattn_f16_noalloc": (_I, [ctypes.POINTER(abi.AlFattnArgs)]),
     "al_last_error": (ctypes.c_char_p, []),

@@ -18,6 +18,7 @@ AL_PREC_DEFAULT = 0
 AL_PREC_F32 = 10
 
 AL_OK = 0
+AL_FATTN_HINT_TAG = 0x31484C41    # "ALH1": op_params i32[4] of an nnml node carrying length hints
 AL_ERR_INVALID = -1
 AL_ERR_UNSUPPORTED = -2
 AL_ERR_HIP = -3

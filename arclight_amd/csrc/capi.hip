@@ -154,6 +154,25 @@ static int library_workspace(size_t bytes, void * stream, void ** ptr) {
     return AL_OK;
 }
 
+extern "C" int al_fattn_release_stream(void * stream) {
+    int dev;
+    DeviceState * st;
+    const int rc = device_state(&dev, &st);
+    if (rc != AL_OK) return rc;
+    std::lock_guard<std::mutex> lk(g_mu);
+    auto it = st->ws.find(stream);
+    if (it == st->ws.end()) return AL_OK;
+    if (it->second.ptr) {
+        // the stream's kernels (and graphs replayed on it) may still use it
+        hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return al_hip_fail(e, "hipDeviceSynchronize");
+        e = hipFree(it->second.ptr);
+        if (e != hipSuccess) return al_hip_fail(e, "hipFree(workspace)");
+    }
+    st->ws.erase(it);
+    return AL_OK;
+}
+
 // ---------------------------------------------------------------------------
 // flash attention
 // ---------------------------------------------------------------------------
@@ -576,12 +595,47 @@ static int fattn_run(const al_fattn_args * a, void * noalloc_ws, size_t noalloc_
 
 extern "C" int al_fattn_f16(const al_fattn_args * a) { return fattn_run(a, nullptr, 0); }
 
+extern "C" int al_fattn_apply_node_hints(al_fattn_args * a, const int32_t * op_params) {
+    if (!a || !op_params || op_params[4] != (int32_t) AL_FATTN_HINT_TAG) return 0;
+    a->kv_len = op_params[5];
+    a->causal_pos0 = op_params[6] < 0 ? -1 : op_params[6];
+    a->mask = al_tensor{};
+    return 1;
+}
+
+// Byte range [lo, hi) an operand's elements span (esz bytes each).
+static void tensor_span(const al_tensor & t, uint64_t esz, uintptr_t * lo, uintptr_t * hi) {
+    uint64_t last = 0;
+    for (int i = 0; i < 4; ++i)
+        if (t.ne[i] > 0) last += (uint64_t) (t.ne[i] - 1) * t.nb[i];
+    *lo = (uintptr_t) t.data;
+    *hi = (uintptr_t) t.data + last + esz;
+}
+
+static bool spans_overlap(const al_tensor & a, uint64_t ea, const al_tensor & b, uint64_t eb) {
+    if (!a.data || !b.data) return false;
+    uintptr_t alo, ahi, blo, bhi;
+    tensor_span(a, ea, &alo, &ahi);
+    tensor_span(b, eb, &blo, &bhi);
+    return alo < bhi && blo < ahi;
+}
+
 extern "C" int al_fattn_f16_with_inputs(const al_attn_inputs_args * in, const al_fattn_args * a) {
     if (!in || !a) return al_fail(AL_ERR_INVALID, "fattn_with_inputs: null arguments");
     DecodeInputs di;
     int mode = 0;
     int rc = attn_inputs_decode(in, &di, &mode);
     if (rc != AL_OK) return rc;
+    // Every workgroup reads the raw inputs while the first split writes
+    // q_out and the new cache rows, so no input may share memory with those
+    // outputs (the pair of calls allows an in-place Q; this launch does not).
+    const al_tensor * inputs[] = {&in->q, &in->q_w, &in->k, &in->k_w, &in->v, &in->pos, &in->rows};
+    const uint64_t in_esz[] = {4, 4, 4, 4, 4, 4, in->rows.type == AL_TYPE_I64 ? 8u : 4u};
+    for (int i = 0; i < 7; ++i)
+        if (spans_overlap(*inputs[i], in_esz[i], in->q_out, 4) || spans_overlap(*inputs[i], in_esz[i], in->k_cache, 2) ||
+            spans_overlap(*inputs[i], in_esz[i], in->v_cache, 2))
+            return al_fail(AL_ERR_UNSUPPORTED, "fattn_with_inputs: an input shares memory with q_out or the caches "
+                           "(in-place operands need al_attn_inputs_f32 then al_fattn_f16)");
     // the attention's query operand is q_out (al_fattn q axes [D, T, Hq, B]),
     // read here from the inputs' raw rows, which the kernel normalizes
     const al_tensor & q = a->q, & qo = in->q_out;
@@ -609,7 +663,9 @@ extern "C" int al_fattn_f16_worker(const al_fattn_args * a, int ith, int nth) {
     if (rc != AL_OK) return rc;
     const hipError_t e = hipStreamSynchronize((hipStream_t) a->stream);
     if (e != hipSuccess) return al_hip_fail(e, "fattn: hipStreamSynchronize");
-    return AL_OK;
+    // errors the kernels recorded (a merge that gave up waiting writes NaN
+    // rows and sets one), reported here as the reference's asserts would stop
+    return al_device_errors();
 }
 
 // ---------------------------------------------------------------------------
@@ -650,11 +706,18 @@ extern "C" int al_fattn_f16_noalloc(const al_fattn_args * a) {
     DeviceState * st;
     int rc = device_state(&dev, &st);
     if (rc != AL_OK) return rc;
-    if (!st->noalloc) {
+    void * scratch_ptr;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        scratch_ptr = st->noalloc;
+    }
+    if (!scratch_ptr) {
         rc = al_fattn_noalloc_init();
         if (rc != AL_OK) return rc;
+        std::lock_guard<std::mutex> lk(g_mu);
+        scratch_ptr = st->noalloc;
     }
-    return fattn_run(a, st->noalloc, AL_FATTN_NOALLOC_SCRATCH_BYTES);
+    return fattn_run(a, scratch_ptr, AL_FATTN_NOALLOC_SCRATCH_BYTES);
 }
 
 extern "C" const char * al_last_error(void) { return g_last_error.c_str(); }

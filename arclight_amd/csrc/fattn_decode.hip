@@ -1,4 +1,4 @@
-// Decode (and short speculative-verify) attention for gfx950: up to 16 query
+// Decode (and short speculative-verify) attention for gfx950: up to 32 query
 // rows per kv head, K/V streamed through LDS a whole cell range at a time.
 // Semantics as nnml_compute_forward_flash_attn_ext_f16
 // (nnml/src/ops/arm/arm.cpp:2196-2433), numerics as fattn_splitkv.hip.
@@ -194,7 +194,6 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     if constexpr (FUSED) {
         for (int i = ws; i < kPieces; i += WS) {
             const char * src;
-            uint32_t bytes = 512;
             if (i == 0) src = in.q_w;
             else if (i == 1) src = in.k_w;
             else if (i == 2) src = in.k + kvh * in.k_nb1;
@@ -637,20 +636,27 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         if (lane == 0) st_agent_u32(flags + split, epoch + 1u);
     }
     if (kidx >= K) return;
+    // A merger that gives up waiting (kFlagPollLimit) records the device
+    // error and writes NaN rows, so that the failure shows in dst as well.
+    int * const merge_failed = (int *) qlds;                           // the query rows are in registers
     if (ws == 0) {
+        int gave_up = 0;
         for (int tries = 0;; ++tries) {
             const unsigned f = lane < p.n_split ? ld_agent_u32(flags + lane) : epoch + 1u;
             if (__all(f == epoch + 1u)) break;
             if (tries >= kFlagPollLimit) {
+                gave_up = 1;
                 if (lane == 0) atomicCAS(p.err + 2, 0, 1);
                 break;
             }
             __builtin_amdgcn_s_sleep(1);
         }
         order_after_counter();
-        if (kidx == 0 && lane == 0) st_agent_u32(flags + 32, epoch + 1u);
+        if (kidx == 0 && lane == 0 && !gave_up) st_agent_u32(flags + 32, epoch + 1u);
+        if (lane == 0) *merge_failed = gave_up;
     }
     __syncthreads();
+    const bool failed = *merge_failed != 0;
 
     // The merge of this merger's n_my rows. The (m, l) pair of every (row,
     // split) is loaded once (thread i takes pairs i, i + 64 WS, ...) and
@@ -740,7 +746,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                 const int t = div_g(rr, p.G, p.g_magic);
                 const int hq = kvh * p.G + rr - t * p.G;
                 float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
-                *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
+                *(float4 *) (out + 4 * d4) =
+                    failed ? float4{__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf("")}
+                           : finalize4(acc, M, L, p.sinks, hq);
             }
         }
     }

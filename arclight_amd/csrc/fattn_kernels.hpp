@@ -62,13 +62,15 @@ size_t fattn_prefill_lds_bytes();
 constexpr int kFattnPrefillRows = 128;          // query rows per workgroup (at most)
 constexpr int kFattnPrefillMaxSplit = 4;        // workgroups sharing one row tile
 
-// Decode kernel: up to 16 query rows per kv head, one kv head per
-// workgroup, `waves` wavefronts each streaming 16-cell stages of K/V through
-// a private ring of `stages` LDS buffers; fattn_decode_config_ok tells which
-// combinations exist. At most kFattnMaxSplit splits per (stream, kv head);
-// with more than one, merge records in the workspace and split flags in its
-// counter region (kFattnDecodeFlagWords per stream x kv head, at most
-// kFattnDecodeFlagUnits of them); min(splits, rows) splits merge.
+// Decode kernel: up to 32 query rows per kv head (17..32 as two row blocks,
+// 8 x 2 only), one kv head per workgroup, `waves` wavefronts each streaming
+// 16-cell stages of K/V through a private ring of `stages` LDS buffers;
+// fattn_decode_config_ok tells which combinations exist. At most
+// kFattnMaxSplit splits per (stream, kv head); with more than one, merge
+// records in the workspace and split flags in its counter region
+// (kFattnDecodeFlagWords per stream x kv head, at most
+// kFattnDecodeFlagUnits of them); min(splits, rows / merge_rows) splits of a
+// unit merge.
 bool fattn_decode_config_ok(int waves, int stages);
 
 // The attention inputs of one layer folded into the decode kernel

@@ -481,8 +481,9 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 // four cells at a time, each group's loads kept in its slot
                 // (a cold path: few registers rather than latency hiding)
                 // (cell c0 + 4 h + off visible when off <= d; the offsets
-                // are immediates of the compares and loads)
-                const int d = lim - c0 - 4 * h;
+                // are immediates of the compares and loads; padding rows of
+                // a ragged last tile load nothing)
+                const int d = (rvalid ? lim : -1) - c0 - 4 * h;
                 const _Float16 * mt = mrow + c0 + 4 * h;
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)

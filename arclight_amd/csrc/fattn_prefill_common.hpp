@@ -1,6 +1,6 @@
-// Pieces shared by the prefill kernels (fattn_prefill.hip: 128-row tiles,
-// fattn_prefill_w64.hip: 64-row tiles), which are compiled with different
-// register-allocation options.
+// Pieces of the prefill kernel (fattn_prefill.hip), whose RG = 4 (128-row
+// tiles) and RG = 2 (64-row tiles, two cell splits per workgroup)
+// instantiations share them.
 #pragma once
 
 #include "fattn_tile.hpp"

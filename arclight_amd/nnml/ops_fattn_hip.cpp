@@ -57,8 +57,12 @@ void nnml_compute_forward_flash_attn_ext_hip(nnml_tensor * node, const nnml_comp
     a.max_bias = node->get_op_params_f32(1);
     a.logit_softcap = node->get_op_params_f32(2);
     a.prec = node->get_op_params_i32(3);
-    a.kv_len = 0;                  // the mask tensor alone decides visibility
+    a.kv_len = 0;                  // the mask tensor alone decides visibility ...
     a.causal_pos0 = -1;
+    // ... unless the graph marked the node: op_params i32[4..6] = tag,
+    // kv_len, causal_pos0, set when the ubatch's mask is exactly that rule
+    // (al_kv_cells_implicit); then the rule replaces the mask
+    al_fattn_apply_node_hints(&a, node->get_operation_params());
     a.stream = nnml_fattn_hip_stream;
     const int rc = al_fattn_f16_worker(&a, params->ith, params->nth);
     if (rc != AL_OK) NNML_ABORT("flash_attn_ext (MI355X): %s", al_last_error());

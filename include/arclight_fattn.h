@@ -86,13 +86,17 @@ typedef struct al_tensor {
  *   - cells c >= kv_len are masked for every query row (kv_len <= 0: n_kv);
  *   - when causal_pos0 >= 0, cell c is masked for query token t when
  *     c > causal_pos0 + t.
- * With a mask tensor present these must agree with it (the nnml shim derives
- * them from the mask it stages); the result is then identical to the
- * explicit mask alone, while wholly masked tiles are skipped unread.
+ * With a mask tensor present these must agree with it; the result is then
+ * identical to the explicit mask alone, while wholly masked tiles are
+ * skipped unread. (The nnml adapter passes the hints, without the mask,
+ * when the node carries them: al_fattn_apply_node_hints below.)
  *
  * workspace: device scratch for split-KV partials. NULL lets the library use
  * its own buffer for the current device and args->stream (allocated on first
- * use, grown when needed; a graph captured on a stream uses that stream's).
+ * use, grown when needed, kept until al_fattn_release_stream; a graph
+ * captured on a stream uses that stream's, so the stream needs one eager call
+ * of the same shapes before the capture: allocating inside a capture fails;
+ * callers that cannot make one use al_fattn_f16_noalloc).
  * A caller workspace must be zero-filled before its first use. Its first
  * 256 KiB hold arrival counters, which every call leaves at zero again, and
  * the decode kernel's split flags, which carry a per-(stream, kv head) epoch
@@ -146,12 +150,42 @@ int al_fattn_f16(const al_fattn_args * args);
  * nnml_single_graph_compute_thread :122-146; nnml/include/thread.h:153-168),
  * splits the rows by ith (nnml/src/ops/arm/arm.cpp:2250-2257), and puts a
  * barrier after the node (scheduler.cpp:135-142). Here worker 0 runs
- * al_fattn_f16 and waits for args->stream, so that barrier still means the
- * output is complete; every other worker returns AL_OK at once without
- * reading args or calling the HIP runtime. (ith, nth) outside
- * 0 <= ith < nth gives AL_ERR_INVALID.
+ * al_fattn_f16, waits for args->stream and returns what al_device_errors
+ * then reports, so that barrier still means the output is complete (or the
+ * node failed); every other worker returns AL_OK at once without reading
+ * args or calling the HIP runtime. (ith, nth) outside 0 <= ith < nth gives
+ * AL_ERR_INVALID.
  */
 int al_fattn_f16_worker(const al_fattn_args * args, int ith, int nth);
+
+/*
+ * Length hints an nnml flash_attn_ext node carries for this library in
+ * op_params i32[4..6], words the reference leaves zero (tensor_new clears
+ * op_params, nnml/src/tensor.cpp:213; the node uses words 0..3,
+ * tensor.cpp:1311, 1334-1338): [4] = AL_FATTN_HINT_TAG, [5] = kv_len,
+ * [6] = causal_pos0 (-1: not causal). The tag states that the node's mask
+ * tensor is exactly the implicit rule of al_fattn_args: the graph sets these
+ * words when al_kv_cells_implicit says so for the ubatch whose mask it fills
+ * (set_inputs_attn_mask, nnml/src/cgraph.cpp:1224-1261), and clears word 4
+ * otherwise. No counterpart in the reference, which always reads the mask.
+ * al_fattn_apply_node_hints: when op_params carries the tag, sets
+ * args->kv_len and args->causal_pos0 from it and drops args->mask (the
+ * implicit rule gives the same results without reading the mask) and
+ * returns 1; otherwise leaves args unchanged and returns 0. NULL arguments
+ * return 0.
+ */
+#define AL_FATTN_HINT_TAG 0x31484c41   /* "ALH1" */
+int al_fattn_apply_node_hints(al_fattn_args * args, const int32_t * op_params);
+
+/*
+ * Frees the library workspace of (current device, stream) that calls with
+ * workspace == NULL made, after waiting for the device (its kernels and any
+ * graph replayed on the stream may still use it). No counterpart in the
+ * reference (its op uses per-thread scratch of the graph's work buffer,
+ * nnml/src/ops/arm/arm.cpp:2299-2302). A later call allocates again. AL_OK
+ * when the stream has none.
+ */
+int al_fattn_release_stream(void * stream);
 
 /* Workspace bytes al_fattn_f16 needs for these arguments (0 if none). */
 uint64_t al_fattn_workspace_bytes(const al_fattn_args * args);
@@ -199,10 +233,11 @@ int al_set_rows_f32_f16(const al_tensor * dst, const al_tensor * src,
 
 /*
  * Reports and clears errors that kernels recorded on the current device
- * (out-of-range set_rows indices: AL_ERR_INVALID; a prefill wave that gave
- * up waiting for its partner wave's tile hand-off, which a correct run
- * never does: AL_ERR_HIP). Call after synchronizing the stream. Returns
- * AL_OK or the error with al_last_error() set.
+ * (out-of-range set_rows indices: AL_ERR_INVALID; a decode merge that gave
+ * up waiting for the other splits of its launch, about a second, which a
+ * correct run never does: AL_ERR_HIP, and that call's merged rows hold
+ * NaN). Call after synchronizing the stream. Returns AL_OK or the error
+ * with al_last_error() set.
  */
 int al_device_errors(void);
 

@@ -243,10 +243,10 @@ def test_shapes_alternating_on_one_workspace(gpu):
     assert not cnt.any(), "arrival counters not left at zero"
 
 
-@pytest.mark.parametrize("pos0", [0, 1536])
+@pytest.mark.parametrize("pos0", [0, 512, 1024, 1536])
 def test_prefill_kernel_chunk512_qwen3_4b(gpu, pos0):
-    # 512-token chunk of a 2048-token causal prefill (Hq 32, Hkv 8): enough
-    # 64-row tiles to take the dedicated prefill kernel
+    # each 512-token chunk of a 2048-token causal prefill (Hq 32, Hkv 8), the
+    # whole output against the oracle
     n_kv = 2048
     q, k, v = O.make_inputs(500 + pos0, T=512, Hq=32, Hkv=8, n_kv=n_kv)
     _check(f"prefill chunk 512 pos0 {pos0}", q, k, v, scale=SCALE, kv_len=pos0 + 512, causal_pos0=pos0)
@@ -283,6 +283,21 @@ def test_prefill_kernel_explicit_masks(gpu):
     mh = np.broadcast_to(O.causal_mask(256, 1024, 700, kv_len=956), (2, 16, 256, 1024)).copy()
     mh[1, 3, :, 200:220] = np.float16(-2.0)
     _check("prefill, per-head general mask, 2 streams", q2, k2, v2, mh, scale=SCALE, max_bias=4.0)
+
+
+def test_prefill_kernel_explicit_masks_ragged_tiles(gpu):
+    # rows per kv head not a multiple of the row tile (T=510 with G=4: 2040
+    # rows; T=300 with G=8: 2400 rows), so the last tile has padding rows, with
+    # a prefix mask (extents) and a mask with holes (the general mode, whose
+    # padding rows must read no mask values)
+    for seed, T, Hq, n_kv, pos0 in ((2111, 510, 32, 1536, 1000), (2112, 300, 64, 1024, 700)):
+        q, k, v = O.make_inputs(seed, T=T, Hq=Hq, Hkv=8, n_kv=n_kv)
+        m = O.causal_mask(T, n_kv, pos0, kv_len=pos0 + T)
+        _check(f"prefill T={T} G={Hq // 8}, ragged last tile, prefix mask", q, k, v, m, scale=SCALE)
+        mh = m.copy()
+        mh[0, 0, 7:T - 3, 50:90] = -np.inf                                # holes: the general mode
+        mh[0, 0, T - 1, 3] = np.float16(-1.5)
+        _check(f"prefill T={T} G={Hq // 8}, ragged last tile, mask with holes", q, k, v, mh, scale=SCALE)
 
 
 def test_prefill_kernel_streams_ragged(gpu):

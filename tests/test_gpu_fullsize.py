@@ -63,6 +63,18 @@ def test_decode_qwen3_32b_ctx32768(gpu):
     assert_parity(run_gpu(q, k, v, scale=SCALE, kv_len=32768), ref, what="decode 32B ctx 32768")
 
 
+def test_decode_qwen3_4b_ctx32768_explicit_mask(gpu):
+    # the benchmark's decode as nnml calls it: the new token at position
+    # 32768 over 32769 valid cells of 33024 (padded to 256), with the f16 mask
+    # tensor (PAD(1, 64) rows) and no length hints
+    n_kv = 33024
+    q, k, v = O.make_inputs(3233, T=1, Hq=32, Hkv=8, n_kv=n_kv)
+    m = O.causal_mask(1, n_kv, 32768, kv_len=32769)
+    _case("decode Qwen3-4B shape ctx 32768, explicit mask")
+    assert_parity(run_gpu(q, k, v, m, scale=SCALE), O.attention(q, k, v, m, scale=SCALE),
+                  what="decode 4B ctx 32768 explicit mask")
+
+
 @pytest.mark.parametrize("pos0", [0, 1024, 2048, 3072])
 def test_prefill_qwen3_32b_chunk1024(gpu, pos0):
     # the four 1024-token chunks of a 4096-token prompt at 64 query heads

@@ -167,3 +167,38 @@ def test_fused_inputs_rejected_shapes(gpu):
         device.synchronize()
         assert np.all(dst.numpy(np.float32) == 7.0)
         assert np.array_equal(kc.numpy(np.uint16), host["kc"])
+
+
+def test_fused_inputs_in_place_query_rejected(gpu):
+    """q_out over the raw query rows (an in-place Q): every split of the
+    fused launch reads the raw rows while split 0 writes q_out, so the call
+    is refused (AL_ERR_UNSUPPORTED, nothing enqueued); the pair of calls
+    takes the in-place operand and matches the out-of-place pair."""
+    from arclight_amd import device, fattn, prologue
+    from arclight_amd._lib import ArclightError
+    _case("fused inputs, in-place query rows (multi-split decode)")
+    T, n_kv, rows = 1, 4096, [4095]
+    host, dev, rope = _setup(13, T, n_kv, rows)
+    out_of_place = _pair_and_fused(host, dev, rope, T, n_kv, kv_len=n_kv, causal_pos0=-1)
+    kc = device.DeviceTensor.from_numpy(host["kc"])
+    vc = device.DeviceTensor.from_numpy(host["vc"])
+    kview = device.DeviceTensor(kc.buf, abi.AL_TYPE_F16, (1, n_kv, Hkv, D), None, 0, abi.KV_AXES)
+    vview = device.DeviceTensor(vc.buf, abi.AL_TYPE_F16, (1, n_kv, Hkv, D), None, 0, abi.KV_AXES)
+    q_inplace = device.DeviceTensor.from_numpy(host["q"])
+    dst = device.DeviceTensor.from_numpy(np.full((1, T, Hq, D), 7.0, np.float32), axes=abi.DST_AXES)
+    with pytest.raises(ArclightError, match="UNSUPPORTED"):
+        prologue.attention_with_inputs(q_inplace, dev["wq"], dev["k"], dev["wk"], dev["v"], dev["pos"], dev["rows"],
+                                       q_inplace, kc, vc, kview, vview, dst, eps=EPS, scale=1 / math.sqrt(D), rope=rope,
+                                       kv_len=n_kv, causal_pos0=-1)
+    device.synchronize()
+    assert np.all(dst.numpy(np.float32) == 7.0)
+    assert np.array_equal(q_inplace.numpy(np.float32), host["q"])
+    # the pair in place
+    prologue.attn_inputs(q_inplace, dev["wq"], dev["k"], dev["wk"], dev["v"], dev["pos"], dev["rows"], q_inplace, kc, vc,
+                         eps=EPS, rope=rope)
+    qv = device.DeviceTensor(q_inplace.buf, abi.AL_TYPE_F32, (1, T, Hq, D), None, 0, abi.Q_AXES)
+    fattn.flash_attn_ext(qv, kview, vview, scale=1 / math.sqrt(D), dst=dst, kv_len=n_kv, causal_pos0=-1)
+    device.synchronize()
+    fattn.device_errors()
+    assert np.array_equal(dst.numpy(np.float32).view(np.uint32), out_of_place["dst"][0].view(np.uint32))
+    assert np.array_equal(q_inplace.numpy(np.float32).view(np.uint32), out_of_place["q_out"][0].view(np.uint32))

@@ -12,7 +12,10 @@ Checks:
   canary buffer, which still holds its fill pattern afterwards;
 - every node's output matches oracle O2 (max-abs <= 2e-3, rel-L2 <= 1e-3).
 Nodes: two decode layers, an explicitly masked decode (the call as nnml
-makes it), a 4-draft verify, and a masked 512-token prefill chunk.
+makes it), a 4-draft verify, a masked 512-token prefill chunk, and the
+masked decode and prefill nodes again carrying the library's length hints
+in op_params i32[4..6] (al_fattn_apply_node_hints, as the nnml adapter
+applies them: the mask is dropped and the implicit rule runs).
 """
 import ctypes
 import math
@@ -37,7 +40,7 @@ def _case(name):
 @pytest.mark.parametrize("nth", [1, 8])
 def test_worker_pool_runs_nodes_like_nnml(gpu, nth):
     from arclight_amd import _lib, abi, device, fattn
-    _lib.load()
+    lib = _lib.load()
     assert os.path.exists(HARNESS), "harness not built (python -c 'import __graft_entry__ as g; g.build()')"
     h = ctypes.CDLL(HARNESS)
     h.al_harness_run_workers.restype = ctypes.c_int
@@ -48,15 +51,23 @@ def test_worker_pool_runs_nodes_like_nnml(gpu, nth):
     keep = []
     nodes, others, refs, dsts, canaries = [], [], [], [], []
 
-    def node(name, q, k, v, mask=None, **kw):
+    def node(name, q, k, v, mask=None, hints=None, **kw):
         dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
         dm = fattn.upload_mask(mask) if mask is not None else None
         dst = device.DeviceTensor.empty(q.shape, np.float32, axes=abi.DST_AXES)
         can = device.DeviceTensor.from_numpy(np.full(q.shape, CANARY, np.uint32).view(np.float32),
                                              axes=abi.DST_AXES)
         keep.extend([dq, dk, dv, dm])
-        nodes.append(fattn.fattn_args(dq, dk, dv, dm, None, dst, scale=SCALE, stream=st, **kw))
-        others.append(fattn.fattn_args(dq, dk, dv, dm, None, can, scale=SCALE, stream=st, **kw))
+        a = fattn.fattn_args(dq, dk, dv, dm, None, dst, scale=SCALE, stream=st, **kw)
+        b = fattn.fattn_args(dq, dk, dv, dm, None, can, scale=SCALE, stream=st, **kw)
+        if hints is not None:
+            op = (ctypes.c_int32 * 16)()
+            op[4], op[5], op[6] = abi.AL_FATTN_HINT_TAG, hints[0], hints[1]
+            assert lib.al_fattn_apply_node_hints(ctypes.byref(a), op) == 1
+            assert lib.al_fattn_apply_node_hints(ctypes.byref(b), op) == 1
+            assert not a.mask.data and a.kv_len == hints[0]
+        nodes.append(a)
+        others.append(b)
         refs.append((name, O.attention(q, k, v, mask, scale=SCALE, **kw)))
         dsts.append(dst)
         canaries.append(can)
@@ -70,6 +81,11 @@ def test_worker_pool_runs_nodes_like_nnml(gpu, nth):
     node("verify 4 drafts", q, k, v, kv_len=4100, causal_pos0=4096)
     q, k, v = O.make_inputs(712, T=512, Hq=32, Hkv=8, n_kv=2048)
     node("prefill chunk 512, explicit mask", q, k, v, O.causal_mask(512, 2048, 1536, kv_len=2048))
+    q, k, v = O.make_inputs(713, T=1, Hq=32, Hkv=8, n_kv=4096)
+    node("decode, explicit mask + node hints", q, k, v, O.causal_mask(1, 4096, 3999, kv_len=4000), hints=(4000, 3999))
+    q, k, v = O.make_inputs(714, T=512, Hq=32, Hkv=8, n_kv=2048)
+    node("prefill chunk 512, explicit mask + node hints", q, k, v, O.causal_mask(512, 2048, 1536, kv_len=2048),
+         hints=(2048, 1536))
 
     n = len(nodes)
     arr = (abi.AlFattnArgs * n)(*nodes)

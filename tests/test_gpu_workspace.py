@@ -191,3 +191,30 @@ def test_split_flags_and_counters_across_calls(gpu):
         flags = words[half:].reshape(-1, 64)[:8]      # the 8 kv heads of stream 0
         assert (flags[:, 32] == epoch).all(), f"{name}: epochs {flags[:, 32]} != {epoch}"
         assert (flags[:, 0] == epoch).all(), f"{name}: split 0 flags {flags[:, 0]} != {epoch}"
+
+
+def test_release_stream_workspace(gpu):
+    """al_fattn_release_stream frees a stream's library workspace: split
+    decode calls on the stream before and after the release (which
+    allocates a new, zeroed workspace) match the oracle; releasing a stream
+    that has none is AL_OK."""
+    from arclight_amd import _lib, device, fattn
+    lib = _lib.load()
+    q, k, v = O.make_inputs(4343, T=1, Hq=32, Hkv=8, n_kv=8192)
+    ref = O.attention(q, k, v, scale=SCALE, kv_len=8000)
+    dq, dk, dv = fattn.upload_q(q), fattn.upload_kv(k), fattn.upload_kv(v)
+    st = device.Stream()
+    try:
+        for rnd in range(3):
+            _case(f"decode on a stream, workspace round {rnd}")
+            for i in range(2):
+                dst = _dst(q)
+                fattn.flash_attn_ext(dq, dk, dv, scale=SCALE, kv_len=8000, dst=dst, stream=st)
+                st.synchronize()
+                fattn.device_errors()
+                assert_parity(dst.numpy(np.float32), ref, what=f"round {rnd} call {i}")
+            assert lib.al_fattn_release_stream(st.handle) == 0, lib.al_last_error()
+        assert lib.al_fattn_release_stream(st.handle) == 0        # nothing left to free
+    finally:
+        device.synchronize()
+        st.destroy()

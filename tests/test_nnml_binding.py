@@ -43,6 +43,7 @@ def test_adapter_compiles_against_nnml_headers(tmp_path):
         syms = subprocess.run([nm, "-C", str(obj)], capture_output=True, text=True, check=True).stdout
         assert "T nnml_compute_forward_flash_attn_ext_hip(nnml_tensor*, nnml_compute_state const*)" in syms
         assert "U al_fattn_f16_worker" in syms
+        assert "U al_fattn_apply_node_hints" in syms
 
 
 def _lib_cpu():
@@ -70,3 +71,31 @@ def test_worker_ids_out_of_range(ith, nth):
     a = abi.AlFattnArgs()
     assert lib.al_fattn_f16_worker(ctypes.byref(a), ith, nth) == abi.AL_ERR_INVALID
     assert b"worker" in lib.al_last_error()
+
+
+def test_node_hints_applied_only_with_the_tag():
+    """al_fattn_apply_node_hints (include/arclight_fattn.h): op_params
+    i32[4..6] = tag, kv_len, causal_pos0 set the implicit rule and drop the
+    mask; without the tag (the reference's nodes: words 4.. are zero) the
+    arguments are left as they are. Host logic only, no GPU."""
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    fn = lib.al_fattn_apply_node_hints
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(abi.AlFattnArgs), ctypes.POINTER(ctypes.c_int32)]
+    a = abi.AlFattnArgs()
+    a.mask.data = ctypes.c_void_p(0x1000)
+    a.kv_len, a.causal_pos0 = 0, -1
+    plain = (ctypes.c_int32 * 16)()                    # a reference node: words 4.. zero
+    assert fn(ctypes.byref(a), plain) == 0
+    assert a.mask.data == 0x1000 and a.kv_len == 0 and a.causal_pos0 == -1
+    hinted = (ctypes.c_int32 * 16)()
+    hinted[4], hinted[5], hinted[6] = abi.AL_FATTN_HINT_TAG, 4097, 4096
+    assert fn(ctypes.byref(a), hinted) == 1
+    assert not a.mask.data and a.kv_len == 4097 and a.causal_pos0 == 4096
+    b = abi.AlFattnArgs()
+    b.mask.data = ctypes.c_void_p(0x2000)
+    hinted[6] = -5                                     # not causal
+    assert fn(ctypes.byref(b), hinted) == 1 and b.causal_pos0 == -1 and b.kv_len == 4097
+    assert fn(None, hinted) == 0 and fn(ctypes.byref(b), None) == 0

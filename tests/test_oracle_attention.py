@@ -243,6 +243,52 @@ def test_arm_faithful_diagnostic_sits_outside_the_parity_bar():
     assert 1e-3 < rel(o3, o1) < 1e-2
 
 
+def _o3_exact_case(seed, equal_scores):
+    """Inputs on which the ARM build's f16 arithmetic is exact: integer q, k
+    and V (small enough that every f16 product and partial sum is an
+    integer below 2048), and either all scores equal (q = 0: every visible
+    cell weighs 1, 32 or 16 visible cells per token, so 1/S is exact) or one
+    cell per kv head whose score (128, scale 1) outweighs the others (0) so
+    far that exp(-128) vanishes in f16 and does not move an f32 result."""
+    rng = np.random.default_rng(seed)
+    T, Hq, Hkv, n_kv, D = 2, 8, 2, 64, 128
+    G = Hq // Hkv
+    q = np.zeros((1, T, Hq, D), np.float32)
+    k = np.zeros((1, n_kv, Hkv, D), np.float16)
+    v = rng.integers(-8, 9, size=(1, n_kv, Hkv, D)).astype(np.float16)
+    mask = np.full((1, 1, 64, n_kv), -np.inf, np.float16)
+    mask[0, 0, 0, 16:48] = 0                      # token 0: 32 visible cells
+    mask[0, 0, 1, 8:24] = 0                       # token 1: 16
+    dominant = {}
+    if not equal_scores:
+        for j in range(Hkv):
+            sign = rng.choice([-1.0, 1.0], size=D).astype(np.float32)
+            q[0, :, j * G:(j + 1) * G, :] = sign        # every head of group j, both tokens
+            d = 20 + 3 * j                              # visible to both tokens
+            k[0, d, j] = sign.astype(np.float16)        # dot 128 against 0 for every other cell
+            dominant[j] = d
+    return q, k, v, mask, dominant
+
+
+@pytest.mark.parametrize("equal_scores", [True, False])
+def test_arm_faithful_equals_exact_where_f16_is_exact(equal_scores):
+    # O3 (the ARM build's f16 dot, f16 rescale and f16 V accumulator) must
+    # equal O1 (float64) exactly where every f16 operation is exact (values,
+    # so -0 equals +0: O1 adds the vanishing weights of the other cells); with
+    # equal scores both are the mean of the visible V rows, with a dominant
+    # cell both are that cell's V row (of the row's own kv head)
+    q, k, v, mask, dominant = _o3_exact_case(31 + equal_scores, equal_scores)
+    o1 = O.attention(q, k, v, mask, scale=1.0, mode="o1")
+    o3 = O.attention(q, k, v, mask, scale=1.0, mode="o3")
+    assert np.array_equal(o3, o1)
+    vf = v.astype(np.float64)
+    for t, (lo, hi) in enumerate(((16, 48), (8, 24))):
+        for h in range(8):
+            j = h // 4
+            want = vf[0, lo:hi, j].mean(axis=0) if equal_scores else vf[0, dominant[j], j]
+            assert np.array_equal(o1[0, t, h], want.astype(np.float32)), (t, h)
+
+
 def test_rejects_what_the_reference_asserts():
     q, k, v = O.make_inputs(17, T=2, Hq=4, Hkv=2, n_kv=32)
     with pytest.raises(ValueError):
