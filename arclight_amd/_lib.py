@@ -55,6 +55,7 @@ SIGNATURES = {
     "al_util_fill_randn_f16": (_I, [_VP, _U64, _U64, _U64, _VP]),
     "al_util_f32_to_f16": (_I, [_VP, _VP, _U64, _VP]),
     "al_util_copy_kernel": (_I, [_VP, _VP, _U64, _VP]),
+    "al_util_empty_launch": (_I, [ctypes.c_int, ctypes.c_int, ctypes.c_int, _VP]),
     # include/arclight_kv.h
     "al_kv_cells_create": (_I, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int32,
                                 ctypes.POINTER(_VP)]),

@@ -132,6 +132,9 @@ __global__ void copy16_kernel(uint4 * __restrict__ dst, const uint4 * __restrict
         dst[i] = src[i];
 }
 
+// Does nothing: launches of it measure the dispatch cost of a grid shape.
+__global__ void empty_kernel() {}
+
 unsigned grid_for(uint64_t n) {
     const uint64_t b = (n + 255) / 256;
     return (unsigned) (b < 8192 ? (b ? b : 1) : 8192);
@@ -169,5 +172,17 @@ extern "C" int al_util_copy_kernel(void * dst, const void * src, uint64_t bytes,
     hipLaunchKernelGGL(copy16_kernel, dim3((unsigned) (blocks < 16384 ? blocks : 16384)), dim3(256), 0,
                        (hipStream_t) stream, (uint4 *) dst, (const uint4 *) src, n16);
     AL_HIP(hipGetLastError(), "copy16 launch");
+    return AL_OK;
+}
+
+extern "C" int al_util_empty_launch(int grid, int block, int lds_bytes, void * stream) {
+    if (grid < 1 || block < 1 || block > 1024 || lds_bytes < 0 || lds_bytes > 160 * 1024)
+        return al_fail(AL_ERR_INVALID, "al_util_empty_launch: grid >= 1, block 1..1024, lds_bytes 0..163840");
+    static const hipError_t attr =
+        hipFuncSetAttribute((const void *) empty_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    AL_HIP(attr, "hipFuncSetAttribute");
+    hipLaunchKernelGGL(empty_kernel, dim3((unsigned) grid), dim3((unsigned) block), (unsigned) lds_bytes,
+                       (hipStream_t) stream);
+    AL_HIP(hipGetLastError(), "empty_kernel launch");
     return AL_OK;
 }

@@ -204,6 +204,21 @@ def bench_prefill(lib, stream, a, T_total=2048, chunk=512, Hq=32, L=None, explic
             "kernel_ms_mean": ms / len(args)}
 
 
+def bench_launch_floor(lib, stream, a, n=144, grid=256, block=512, lds=160 * 1024):
+    """n launches of an empty kernel with the 512-token prefill chunk's launch
+    shape (grid workgroups of block threads holding lds bytes of LDS), replayed
+    as one graph: the dispatch cost per launch that every prefill call pays,
+    and, under a tracer, the tracer's own per-dispatch overhead."""
+    from arclight_amd._lib import call
+
+    def enqueue():
+        for _ in range(n):
+            call("al_util_empty_launch", grid, block, lds, stream.handle)
+
+    ms = time_graph(lib, stream, None, a.steps, a.warmup, enqueue=enqueue)
+    return {"launches": n, "grid": grid, "block": block, "lds_bytes": lds, "us_per_launch": ms * 1e3 / n}
+
+
 def bench_other_configs(lib, stream, a):
     """The remaining workloads of the metric's family, one line each: decode
     at 4K and 16K, speculative verify at 8K context with 4 and 8 drafts
@@ -471,7 +486,9 @@ def main():
         print(json.dumps({"copy": bench_copy(stream)}))
         return
     if a.only == "prefill":
-        print(json.dumps({"prefill": bench_prefill(lib, stream, a)}))
+        print(json.dumps({"prefill": bench_prefill(lib, stream, a),
+                          "prefill_explicit_mask": bench_prefill(lib, stream, a, explicit_mask=True),
+                          "launch_floor": bench_launch_floor(lib, stream, a)}))
         return
     if a.only == "step":
         out = {}

@@ -63,6 +63,12 @@ int al_util_f32_to_f16(uint16_t * dst, const float * src, uint64_t n, void * str
  * hardware byte counters. */
 int al_util_copy_kernel(void * dst, const void * src, uint64_t bytes, void * stream);
 
+/* One launch of a kernel that does nothing, with `grid` workgroups of `block`
+ * threads and `lds_bytes` of dynamic LDS (at most 160 KiB): graphs of such
+ * launches measure the dispatch floor of a grid shape and a tracer's
+ * per-dispatch overhead. */
+int al_util_empty_launch(int grid, int block, int lds_bytes, void * stream);
+
 #ifdef __cplusplus
 }
 #endif
