@@ -434,11 +434,15 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // 2 ks + h) and V^T operand (cell 16 kk + 4 h + (s16 >> 2) [+ 8],
         // granule 4 db + 2 (q16 & 1) + ((s16 & 3) >> 1), half s16 & 1, for
         // 16-lane group q16)
-        const int q16 = (lane >> 4) & 3, s16 = lane & 15;
-        const int vcell = 4 * h + (s16 >> 2);
-        const int vgran = 2 * (q16 & 1) + ((s16 & 3) >> 1);
-        const int vhalf = (s16 & 1) * 8;
-        const int vsw = 4 * (s16 >> 2);                   // 4 (cell & 3)
+        int vcell, vgran, vhalf, vsw;
+        auto v_offsets = [&](const int ln) {
+            const int q16 = (ln >> 4) & 3, s16 = ln & 15;
+            vcell = 4 * ((ln >> 5) & 1) + (s16 >> 2);
+            vgran = 2 * (q16 & 1) + ((s16 & 3) >> 1);
+            vhalf = (s16 & 1) * 8;
+            vsw = 4 * (s16 >> 2);                         // 4 (cell & 3)
+        };
+        v_offsets(lane);
 
 #pragma unroll
         for (int db = 0; db < 4; ++db) o[db] = floatx16{};
@@ -469,10 +473,18 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // always does)
         auto prepare = [&](floatx16 (&sc)[2], const int c0) {
             if constexpr (SOFTCAP) {
+                // softcap tanh(s scale), eight values at a time (the
+                // exponentials of a whole tile at once would need 32 more
+                // registers than the loop has)
+                const float c2 = 2.0f * kLog2e * p.scale;
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) sc[cb][v] = p.softcap * tanhf(sc[cb][v] * p.scale);
+                    for (int v0 = 0; v0 < 16; v0 += 8) {
+#pragma unroll
+                        for (int v = v0; v < v0 + 8; ++v) sc[cb][v] = p.softcap * tanh_exp2(sc[cb][v], c2);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
             }
             if constexpr (GEN) {
                 // s + slope * mask in the units the scores are kept in (raw
@@ -654,6 +666,11 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 iteration(i, s0, s1);
                 iteration(i + 1, s1, s0);
             }
+            // the loop's last iterations with offsets derived anew from an
+            // opaque lane: the loop's own are not kept live past it
+            int ln = lane;
+            asm volatile("" : "+v"(ln));
+            v_offsets(ln);
             if (i + 1 < NI) {
                 iteration(i, s0, s1);
                 ++i;
@@ -670,11 +687,15 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     }
     float m_nat = m_run == -AL_INF ? -AL_INF : m_run * (cexp / kLog2e);
     float l_row = pair_sum(l_run);
+    // The epilogue's row (an opaque copy: its LDS offsets are computed here,
+    // not hoisted above the loop and held in registers across it)
+    int rre = rr;
+    asm volatile("" : "+v"(rre));
 
     // The splits within the workgroup merge through LDS: split 1 stores its
     // rows' state as a record [row][132], split 0 combines it with its own.
     if constexpr (S::SP == 2) {
-        float * rec = (float *) lds + rr * kRowStride;
+        float * rec = (float *) lds + rre * kRowStride;
         if (!producer && si == 1) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
@@ -688,7 +709,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     }
     const bool owner = !producer && si == 0;               // holds the workgroup's merged rows
     if (S::SP == 2 && owner) {
-        const float * rec = (const float *) lds + rr * kRowStride;
+        const float * rec = (const float *) lds + rre * kRowStride;
         const float2 ml = *(const float2 *) (rec + 128);
         const float M = fmaxf(m_nat, ml.x);
         const float Mu = M == -AL_INF ? 0.0f : M;
@@ -716,14 +737,14 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     if (p.n_split == 1) {
         float * stage = (float *) (lds + 80 * 1024);
         if (owner && rvalid) {
-            const int hq = kvh * p.G + (row0 + rr) - tok_of(row0 + rr) * p.G;
+            const int hq = kvh * p.G + (row0 + rre) - tok_of(row0 + rre) * p.G;
             const RowScale rs = row_scale(m_nat, l_row, p.sinks, hq);
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq) {
                     const int g = 8 * db + 2 * bq + h;
-                    *(float4 *) (stage + rr * 128 + 4 * (g ^ (rr & 31))) =
+                    *(float4 *) (stage + rre * 128 + 4 * (g ^ (rre & 31))) =
                         apply_scale(float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]}, rs);
                 }
         }
@@ -760,10 +781,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq) {
                     const int g = 8 * db + 2 * bq + h;
-                    *(float4 *) (stage + rr * 128 + 4 * (g ^ (rr & 31))) =
+                    *(float4 *) (stage + rre * 128 + 4 * (g ^ (rre & 31))) =
                         float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
                 }
-            if (h == 0) ml_stage[rr] = float2{m_nat, l_row};
+            if (h == 0) ml_stage[rre] = float2{m_nat, l_row};
         }
         __syncthreads();
         for (int i = threadIdx.x; i < rows_here * kGran; i += 2 * kWaves * 64) {

@@ -32,6 +32,15 @@ __device__ __forceinline__ float pair_sum(float x) {
     return __builtin_bit_cast(float, (int) r[0]) + __builtin_bit_cast(float, (int) r[1]);
 }
 
+// tanh(x / c2 * 2 log2 e) = 1 - 2 / (2^(c2 x) + 1), with the hardware exp2
+// and reciprocal: an absolute error of a few 1e-7 (and -1 / +1 exactly where
+// 2^(c2 x) underflows to 0 or overflows to inf) in four instructions and no
+// extra registers, so that the logit softcap keeps the slot-scheduled loop
+// out of scratch. c2 = 2 log2(e) times the factor applied before tanh.
+__device__ __forceinline__ float tanh_exp2(float x, float c2) {
+    return 1.0f - 2.0f * __builtin_amdgcn_rcpf(__builtin_amdgcn_exp2f(x * c2) + 1.0f);
+}
+
 // Waits until at most N LDS-DMA / vector memory instructions of this wave are
 // outstanding.
 template <int N>
