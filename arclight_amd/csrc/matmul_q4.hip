@@ -84,7 +84,7 @@ __device__ __forceinline__ float dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
 }
 constexpr int kQuadXor1 = 0xB1, kQuadXor2 = 0x4E, kRowHalfMirror = 0x141, kRowMirror = 0x140, kRowBcast15 = 0x142,
-              kRowBcast31 = 0x143;
+              kRowBcast31 = 0x143, kRowRor8 = 0x128;
 
 // Sum over the wavefront; the total is valid in lane 63 only.
 __device__ __forceinline__ float wave_sum_to_last(float v) {
@@ -168,36 +168,70 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const char * __restrict__ 
 // Eight values of a Q8_0 block (part 0..3 of it, the four parts in the four
 // lanes of a quad) quantized into LDS.
 __device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, const int part, int8_t * qdst,
-                                              float * ddst, int * sdst) {
+                                              float2 * sdst) {
     const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
     float amax = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
     amax = fmaxf(amax, dpp<kQuadXor1>(amax));
     amax = fmaxf(amax, dpp<kQuadXor2>(amax));
-    const float d = amax / 127.0f;
+    // d = amax / 127 as the IEEE division rounds it: amax r with r = RN(1/127)
+    // and one FMA correction, which gives the correctly rounded quotient for
+    // every finite non-negative float (all 2^31 checked against the division);
+    // an infinite amax passes through as the division would give it
+    constexpr float kR127 = 1.0f / 127.0f;
+    const float q0 = amax * kR127;
+    const float dq = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), kR127, q0);
+    const float d = amax <= 3.40282347e+38f ? dq : amax;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     int sum = 0;
     uint32_t words[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        uint32_t wv = 0;
+        int q[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int q = (int) rintf(v[4 * j + k] * id);                // ties to even, as vcvtnq
-            sum += q;
-            wv |= (uint32_t) (q & 0xff) << (8 * k);
+            q[k] = (int) rintf(v[4 * j + k] * id);                      // ties to even, as vcvtnq
+            sum += q[k];
         }
-        words[j] = wv;
+        // the four low bytes into one word (v_perm: bytes of q0, q1 | of q2, q3)
+        words[j] = __builtin_amdgcn_perm((uint32_t) q[1], (uint32_t) q[0], 0x0c0c0400u) |
+                   __builtin_amdgcn_perm((uint32_t) q[3], (uint32_t) q[2], 0x04000c0cu);
     }
     float fs = (float) sum;                                             // |sum| <= 1016: exact in f32
     fs += dpp<kQuadXor1>(fs);
     fs += dpp<kQuadXor2>(fs);
     *(uint2 *) qdst = uint2{words[0], words[1]};
-    if (part == 0) {
-        *ddst = (float) (_Float16) d;                                   // the block scale as stored (f16)
-        *sdst = (int) fs;
+    if (part == 0) *sdst = float2{(float) (_Float16) d, fs};           // the block scale as stored (f16), the sum
+}
+
+// Eight per-lane values (tokens 0..7) summed over the wavefront, scattered:
+// token t's total ends in lanes 8t .. 8t + 7. Lanes exchange half of their
+// values with lane ^ 32, then ^ 16 (permlane swaps), then ^ 8 (DPP row
+// rotate), each time keeping the tokens of their side, then sum within
+// their 8 lanes: 18 instructions instead of a wave sum per token.
+__device__ __forceinline__ float wave_sum8_scatter(const float (&v)[8], const int lane) {
+    float a[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {       // lanes 0..31 keep tokens k, lanes 32..63 tokens 4 + k
+        const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, v[k]), __builtin_bit_cast(int, v[4 + k]),
+                                                        false, false);
+        a[k] = __builtin_bit_cast(float, (int) r[0]) + __builtin_bit_cast(float, (int) r[1]);
     }
+    float b[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {       // lane bit 4 clear keeps a[k], set keeps a[k + 2]
+        const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, a[k]), __builtin_bit_cast(int, a[k + 2]),
+                                                        false, false);
+        b[k] = __builtin_bit_cast(float, (int) r[0]) + __builtin_bit_cast(float, (int) r[1]);
+    }
+    const bool odd = (lane & 8) != 0;   // lane bit 3 set keeps b[1]
+    const float keep = odd ? b[1] : b[0], send = odd ? b[0] : b[1];
+    float c = keep + dpp<kRowRor8>(send);
+    c += dpp<kQuadXor1>(c);
+    c += dpp<kQuadXor2>(c);
+    c += dpp<kRowHalfMirror>(c);
+    return c;
 }
 
 // One launch for decode and verify (T <= TMAX): every workgroup issues its
@@ -205,7 +239,8 @@ __device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, 
 // (they are small and L2-resident after the first workgroup touches them;
 // each thread issues the loads of all T tokens of its part of a block before
 // using any), then runs the dot products of gemv_q4_kernel from LDS. One
-// wavefront per row.
+// wavefront per row; with several tokens the rows' per-lane sums of all of
+// them meet in one scattering wave reduction.
 template <int BPL, int TMAX>
 __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int64_t w_nb1, int N, int K,
                                                              const char * x, int64_t x_nb1, int T,
@@ -214,11 +249,20 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
     prefetch_params(w_nb1, y_nb1, blockDim.x);
     const int nb = K / 32;
     int8_t * qs = (int8_t *) lds;                                       // [T][K]
-    float * dx = (float *) (lds + T * K);                               // [T][nb]
-    int * sy = (int *) (lds + T * K + 4 * T * nb);                      // [T][nb]
+    float2 * sc = (float2 *) (lds + T * K);                             // [T][nb]: (block scale, value sum)
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int b0 = lane * BPL;
+    // LDS holds block b at slot (b % BPL) * 64 + b / BPL, so that the dot
+    // products' reads (lane l, its j-th block) are lane-consecutive
+    auto block_at = [](const int slot) { return (slot & 63) * BPL + (slot >> 6); };
+    auto load_weights = [&](uint32_t (&c)[9 * BPL / 2]) {
+        const int r = row < N ? row : N - 1;
+        const uint32_t * wr = (const uint32_t *) (w + (int64_t) r * w_nb1 + (int64_t) b0 * 18);
+#pragma unroll
+        for (int i = 0; i < 9 * BPL / 2; ++i) c[i] = wr[i];           // (non-temporal loads measured slower)
+    };
+    uint32_t c[9 * BPL / 2];
 
     // (block, part) items of the activations, a uniform number of rounds per
     // thread; loads are unconditional (indices clamped in bounds) so that no
@@ -227,10 +271,6 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
     const int rounds = (items + blockDim.x - 1) / blockDim.x;
     constexpr int PRE = TMAX == 1 ? 2 : 1;                             // rounds whose loads go out first
     float4 f[PRE][TMAX][2];
-    // LDS holds block b at slot (b % BPL) * 64 + b / BPL, so that the dot
-    // products' reads (lane l, its j-th block) are lane-consecutive; item i
-    // is part i % 4 of the block in slot i / 4
-    auto block_at = [](const int slot) { return (slot & 63) * BPL + (slot >> 6); };
     auto load_item = [&](const int item, float4 (&g)[TMAX][2]) {
         const int it = item < items ? item : items - 1;
         const int b = block_at(it >> 2), part = it & 3;
@@ -247,7 +287,7 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
             const int sl = item >> 2, part = item & 3;
 #pragma unroll
             for (int t = 0; t < TMAX; ++t)
-                if (t < T) quantize_part(g[t][0], g[t][1], part, qs + t * K + 32 * sl + 8 * part, dx + t * nb + sl, sy + t * nb + sl);
+                if (t < T) quantize_part(g[t][0], g[t][1], part, qs + t * K + 32 * sl + 8 * part, sc + t * nb + sl);
         }
     };
     // the first rounds' activations (L2) before the weights (HBM): the
@@ -255,13 +295,7 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
 #pragma unroll
     for (int k = 0; k < PRE; ++k) load_item(threadIdx.x + k * blockDim.x, f[k]);
     asm volatile("" ::: "memory");                                     // keeps the issue order
-    uint32_t c[9 * BPL / 2];
-    {
-        const int r = row < N ? row : N - 1;
-        const uint32_t * wr = (const uint32_t *) (w + (int64_t) r * w_nb1 + (int64_t) b0 * 18);
-#pragma unroll
-        for (int i = 0; i < 9 * BPL / 2; ++i) c[i] = wr[i];           // (non-temporal loads measured slower)
-    }
+    load_weights(c);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int k = 0; k < PRE; ++k)
@@ -285,13 +319,15 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
             hi[j][i] = (q[i] >> 4) & 0x0f0f0f0fu;
         }
     }
-    for (int t = 0; t < T; ++t) {
+    // the row's dot product with token t's activations (this lane's blocks)
+    auto dot_t = [&](const int t) {
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < BPL; ++j) {
             const int sl = j * 64 + lane;                                // block b0 + j
             const uint4 * ab = (const uint4 *) (qs + t * K + 32 * sl);
             const uint4 a0 = ab[0], a1 = ab[1];
+            const float2 s2 = sc[t * nb + sl];
             const uint32_t a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
             int dot = 0;
 #pragma unroll
@@ -299,11 +335,23 @@ __global__ __launch_bounds__(1024) void gemv_q4_fused_kernel(const char * w, int
                 dot = __builtin_amdgcn_sdot4((int) lo[j][i], (int) a[i], dot, false);
                 dot = __builtin_amdgcn_sdot4((int) hi[j][i], (int) a[4 + i], dot, false);
             }
-            const int sumi = dot - 8 * sy[t * nb + sl];
-            part += ((float) sumi * dw[j]) * dx[t * nb + sl];
+            const int sumi = dot - 8 * (int) s2.y;
+            part += ((float) sumi * dw[j]) * s2.x;
         }
-        part = wave_sum_to_last(part);
-        if (lane == 63) *(float *) (y + (int64_t) t * y_nb1 + (int64_t) row * 4) = part;
+        return part;
+    };
+    if constexpr (TMAX == 8) {
+        float part[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) part[t] = t < T ? dot_t(t) : 0.0f;
+        const float tot = wave_sum8_scatter(part, lane);
+        const int t = lane >> 3;
+        if ((lane & 7) == 0 && t < T) *(float *) (y + (int64_t) t * y_nb1 + (int64_t) row * 4) = tot;
+    } else {
+        for (int t = 0; t < T; ++t) {
+            const float part = wave_sum_to_last(dot_t(t));
+            if (lane == 63) *(float *) (y + (int64_t) t * y_nb1 + (int64_t) row * 4) = part;
+        }
     }
 }
 

@@ -66,17 +66,22 @@ def test_wo_matches_oracle(gpu, K, N, T):
     assert rel < 1e-6, rel
 
 
-@pytest.mark.parametrize("K,N,T", [(4096, 301, 1), (8192, 77, 9)])
+@pytest.mark.parametrize("K,N,T", [(4096, 301, 1), (4096, 301, 2), (4096, 301, 8), (8192, 77, 5), (8192, 77, 9)])
 def test_wo_unit_scales_bit_exact(gpu, K, N, T):
     """Unit weight scales and activations whose every block has step 1:
     the result is the integer dot product, which both sides must hit
-    exactly; half-integer activations check the device's ties-to-even."""
+    exactly; half-integer activations check the device's ties-to-even.
+    T = 1 (quarter blocks per thread), 2..8 (whole blocks per thread, one
+    launch) and 9 (the quantization launch) each quantize differently; a
+    block of zeros and one of negative zeros (scale 0) are among them."""
     _case(f"wo exact K={K} N={N} T={T}")
     rng = np.random.default_rng(N + T)
     w = O.random_q4_0(rng, N, K)
     w["d"] = np.float16(1.0).view(np.uint16)
     x = (rng.integers(-253, 254, size=(T, K)) / 2.0).astype(np.float32)
     x[:, ::32] = 127.0
+    x[T - 1, 32:64] = 0.0
+    x[0, 96:128] = -0.0
     got = _run(w, x, x_pad=4, y_pad=3)
     want = O.mul_mat_q4_0(w, x)
     assert np.array_equal(got, want)
