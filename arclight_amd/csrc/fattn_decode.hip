@@ -52,6 +52,22 @@ namespace {
 using namespace fattn;
 
 constexpr int kSC = 16;                                   // cells per stage
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// The largest x of each aligned group of 32 lanes, in all of them: DPP
+// within rows of 16 lanes (lane ^ 1, ^ 2, then the mirrors within 8 and
+// 16), then the group's two rows through a permlane swap.
+__device__ __forceinline__ float max32(float x) {
+    x = fmaxf(x, dpp_f<0xB1>(x));
+    x = fmaxf(x, dpp_f<0x4E>(x));
+    x = fmaxf(x, dpp_f<0x141>(x));
+    x = fmaxf(x, dpp_f<0x140>(x));
+    const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, x), __builtin_bit_cast(int, x), false, false);
+    return fmaxf(__builtin_bit_cast(float, (int) r[0]), __builtin_bit_cast(float, (int) r[1]));
+}
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // FM < 0: the query rows come ready in p.q; FM >= 0: the attention inputs
@@ -659,8 +675,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const bool failed = *merge_failed != 0;
 
     // The merge of this merger's n_my rows. The (m, l) pair of every (row,
-    // split) is loaded once (thread i takes pairs i, i + 64 WS, ...) and
-    // shared through LDS; the output items are two adjacent lanes per (row,
+    // split) is loaded once (thread i takes pairs i, i + 64 WS, ...), turned
+    // into the split's weight and shared through LDS; the output items are two adjacent lanes per (row,
     // 4 dims), each taking 16 of the at most 32 splits and then combining
     // with its partner (split half 0 first, on both lanes). The first
     // round's O loads are issued before the pairs go to LDS, so a merger of
@@ -671,6 +687,11 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     constexpr int kItems = RB == 1 ? 2 : 1;                            // items per thread and round (registers)
     constexpr int kPairs = (16 * RB * kMaxSplit + WS * 64 - 1) / (WS * 64);
     float2 * ml_s = (float2 *) &lds[0][0][0];                          // [local row][kMaxSplit]; the rings are free
+    float * m_row = (float *) (ml_s + 16 * RB * kMaxSplit);            // [local row]
+    // the splits' weights once per (row, split) rather than per item: pays
+    // off with the 8-wave shape's rows per merger (4-draft verify 15.1 ->
+    // 14.3 us at 8K cells), not with the 2-wave decode (+0.1 us at 4K)
+    constexpr bool kWeightsOnce = WS > 2;
     // (loads are unconditional, from clamped in-range addresses, and the
     // unused ones are replaced afterwards: no branch, so the O loads below
     // stay in flight while the pairs are stored)
@@ -704,11 +725,26 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             }
         }
         if (base == 0) {
-            // the pairs into LDS (LDS only: no wait for the O loads in flight)
+            // the pairs into LDS (LDS and lane exchanges only: no wait for the
+            // O loads in flight). With weights_once, as (weight, l), weight =
+            // e^(m - M) with M the row's largest m over its splits (a row's
+            // kMaxSplit pairs are adjacent lanes of one wave), and the row
+            // maxima beside them, so that the items below only multiply and
+            // add; else as (m, l), every item taking its row's maximum and
+            // weights itself
 #pragma unroll
             for (int i = 0; i < kPairs; ++i) {
                 const int pi = i * WS * 64 + threadIdx.x;
-                ml_s[pi] = (pi % kMaxSplit) < p.n_split ? mlv[i] : float2{-AL_INF, 0.0f};
+                const float2 v = (pi % kMaxSplit) < p.n_split ? mlv[i] : float2{-AL_INF, 0.0f};
+                if constexpr (kWeightsOnce) {
+                    static_assert(kMaxSplit == 32, "a row's pairs are the 32 lanes max32 reduces");
+                    const float M = max32(v.x);
+                    const float Mu = (M == -AL_INF) ? 0.0f : M;
+                    ml_s[pi] = float2{exp_fast(v.x - Mu), v.y};
+                    if (pi % kMaxSplit == 0) m_row[pi / kMaxSplit] = M;
+                } else {
+                    ml_s[pi] = v;
+                }
             }
             mem_barrier();
             __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0)
@@ -721,20 +757,27 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
             const int lr = idx < n_items ? idx >> 6 : 0;
-            float2 ml[kHalf];
+            float2 wl[kHalf];                                          // (weight or m, l) of its splits
 #pragma unroll
-            for (int j = 0; j < kHalf; ++j) ml[j] = ml_s[lr * kMaxSplit + half * kHalf + j];
-            float Mh = ml[0].x;
+            for (int j = 0; j < kHalf; ++j) wl[j] = ml_s[lr * kMaxSplit + half * kHalf + j];
+            float M;
+            if constexpr (kWeightsOnce) {
+                M = m_row[lr];
+            } else {
+                float Mh = wl[0].x;
 #pragma unroll
-            for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, ml[j].x);
-            const float M = fmaxf(Mh, __shfl_xor(Mh, 1));
-            const float Mu = (M == -AL_INF) ? 0.0f : M;
+                for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, wl[j].x);
+                M = fmaxf(Mh, __shfl_xor(Mh, 1));
+                const float Mu = (M == -AL_INF) ? 0.0f : M;
+#pragma unroll
+                for (int j = 0; j < kHalf; ++j) wl[j].x = exp_fast(wl[j].x - Mu);
+            }
             float Lh = 0.0f;
             float4 ah = {0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) {
-                const float w = exp_fast(ml[j].x - Mu);
-                Lh += w * ml[j].y;
+                const float w = wl[j].x;
+                Lh += w * wl[j].y;
                 ah.x += w * ov[it2][j].x; ah.y += w * ov[it2][j].y; ah.z += w * ov[it2][j].z; ah.w += w * ov[it2][j].w;
             }
             const float Lo = __shfl_xor(Lh, 1);
