@@ -688,10 +688,6 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     constexpr int kPairs = (16 * RB * kMaxSplit + WS * 64 - 1) / (WS * 64);
     float2 * ml_s = (float2 *) &lds[0][0][0];                          // [local row][kMaxSplit]; the rings are free
     float * m_row = (float *) (ml_s + 16 * RB * kMaxSplit);            // [local row]
-    // the splits' weights once per (row, split) rather than per item: pays
-    // off with the 8-wave shape's rows per merger (4-draft verify 15.1 ->
-    // 14.3 us at 8K cells), not with the 2-wave decode (+0.1 us at 4K)
-    constexpr bool kWeightsOnce = WS > 2;
     // (loads are unconditional, from clamped in-range addresses, and the
     // unused ones are replaced afterwards: no branch, so the O loads below
     // stay in flight while the pairs are stored)
@@ -725,26 +721,22 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             }
         }
         if (base == 0) {
-            // the pairs into LDS (LDS and lane exchanges only: no wait for the
-            // O loads in flight). With weights_once, as (weight, l), weight =
-            // e^(m - M) with M the row's largest m over its splits (a row's
-            // kMaxSplit pairs are adjacent lanes of one wave), and the row
-            // maxima beside them, so that the items below only multiply and
-            // add; else as (m, l), every item taking its row's maximum and
-            // weights itself
+            // the pairs into LDS as (weight, l), weight = e^(m - M) with M the
+            // row's largest m over its splits (a row's kMaxSplit pairs are
+            // adjacent lanes of one wave), and the row maxima beside them, so
+            // that the items below only multiply and add; once per (row,
+            // split) of this merger's rows instead of once per item (LDS and
+            // lane exchanges only: no wait for the O loads in flight)
+            static_assert(kMaxSplit == 32, "a row's pairs are the 32 lanes max32 reduces");
 #pragma unroll
             for (int i = 0; i < kPairs; ++i) {
+                if (i * WS * 64 >= n_my * kMaxSplit) break;               // past this merger's rows (uniform)
                 const int pi = i * WS * 64 + threadIdx.x;
                 const float2 v = (pi % kMaxSplit) < p.n_split ? mlv[i] : float2{-AL_INF, 0.0f};
-                if constexpr (kWeightsOnce) {
-                    static_assert(kMaxSplit == 32, "a row's pairs are the 32 lanes max32 reduces");
-                    const float M = max32(v.x);
-                    const float Mu = (M == -AL_INF) ? 0.0f : M;
-                    ml_s[pi] = float2{exp_fast(v.x - Mu), v.y};
-                    if (pi % kMaxSplit == 0) m_row[pi / kMaxSplit] = M;
-                } else {
-                    ml_s[pi] = v;
-                }
+                const float M = max32(v.x);
+                const float Mu = (M == -AL_INF) ? 0.0f : M;
+                ml_s[pi] = float2{exp_fast(v.x - Mu), v.y};
+                if (pi % kMaxSplit == 0) m_row[pi / kMaxSplit] = M;
             }
             mem_barrier();
             __builtin_amdgcn_s_waitcnt(0xC07F);                        // lgkmcnt(0)
@@ -757,21 +749,10 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             const int half = idx & 1;
             const int d4 = (idx >> 1) & 31;
             const int lr = idx < n_items ? idx >> 6 : 0;
-            float2 wl[kHalf];                                          // (weight or m, l) of its splits
+            float2 wl[kHalf];                                          // (weight, l) of its splits
 #pragma unroll
             for (int j = 0; j < kHalf; ++j) wl[j] = ml_s[lr * kMaxSplit + half * kHalf + j];
-            float M;
-            if constexpr (kWeightsOnce) {
-                M = m_row[lr];
-            } else {
-                float Mh = wl[0].x;
-#pragma unroll
-                for (int j = 1; j < kHalf; ++j) Mh = fmaxf(Mh, wl[j].x);
-                M = fmaxf(Mh, __shfl_xor(Mh, 1));
-                const float Mu = (M == -AL_INF) ? 0.0f : M;
-#pragma unroll
-                for (int j = 0; j < kHalf; ++j) wl[j].x = exp_fast(wl[j].x - Mu);
-            }
+            const float M = m_row[lr];
             float Lh = 0.0f;
             float4 ah = {0, 0, 0, 0};
 #pragma unroll
