@@ -692,6 +692,45 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
     int rre = rr;
     asm volatile("" : "+v"(rre));
 
+    // One workgroup per row tile and two cell splits in it: both splits put
+    // their rows' states into LDS records [split][row][132] at once, then
+    // every thread combines the two states of the 16-byte granules of the
+    // rows it stores, scales them and stores whole rows, 16 bytes per lane,
+    // non-temporal (one pass: no combine by split 0 alone and no staging
+    // copy; the same arithmetic as the merge below).
+    if (S::SP == 2 && p.n_split == 1) {
+        if (!producer) {
+            float * rec = (float *) lds + (si * ROWS + rre) * kRowStride;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int bq = 0; bq < 4; ++bq)
+                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * h) =
+                        float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
+            if (h == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
+        }
+        __syncthreads();
+        for (int item = threadIdx.x; item < rows_here * 32; item += 2 * kWaves * 64) {
+            const int r = item >> 5, g = item & 31;
+            const float * r0 = (const float *) lds + r * kRowStride;
+            const float * r1 = (const float *) lds + (ROWS + r) * kRowStride;
+            const float2 ml0 = *(const float2 *) (r0 + 128), ml1 = *(const float2 *) (r1 + 128);
+            const float M = fmaxf(ml0.x, ml1.x);
+            const float Mu = M == -AL_INF ? 0.0f : M;
+            const float wa = exp_fast(ml0.x - Mu), wb = exp_fast(ml1.x - Mu);
+            const float4 x0 = *(const float4 *) (r0 + 4 * g), x1 = *(const float4 *) (r1 + 4 * g);
+            const float4 o4 = {x0.x * wa + x1.x * wb, x0.y * wa + x1.y * wb, x0.z * wa + x1.z * wb,
+                               x0.w * wa + x1.w * wb};
+            const float L = ml0.y * wa + ml1.y * wb;
+            const int rg_ = row0 + r;
+            const int tk = tok_of(rg_), hq = kvh * p.G + rg_ - tk * p.G;
+            float * out = (float *) (p.dst + ((int64_t) (b * p.T + tk) * p.Hq + hq) * p.dst_nb1);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, apply_scale(o4, row_scale(M, L, p.sinks, hq))),
+                                                   make_rsrc(out, 512), 16 * g, 0, kNonTemporal);
+        }
+        return;
+    }
+
     // The splits within the workgroup merge through LDS: split 1 stores its
     // rows' state as a record [row][132], split 0 combines it with its own.
     if constexpr (S::SP == 2) {
