@@ -542,18 +542,25 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             return half8{a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
         };
 
-        // Iteration i in two phases of explicitly ordered slots (each slot:
+        // Iteration i in eight explicitly ordered slots and a tail (each slot:
         // the LDS reads it prefetches, then its vector work and MFMAs;
         // nothing moves across slots):
-        // A: S(i + 1) = K(i + 1) Q^T on the matrix cores (eight slots of two
-        //    MFMAs, K operands read two slots ahead) while the vector ALU
-        //    turns S(i) into unnormalised probabilities p = exp2(s c - m c),
-        //    rounded to f16 (RNE) into the P^T operands; the first V
-        //    operands are read in the last slot.
-        // B: O^T += V(i)^T P(i)^T and the row sums of the f16 probabilities
-        //    (four slots of four MFMAs, V operands read one slot ahead).
-        // P^T operand kk holds cells 16 kk .. 16 kk + 15, i.e. registers
-        // 8 (kk & 1) .. + 7 of S^T block kk / 2.
+        // - S(i + 1) = K(i + 1) Q^T on the matrix cores, two MFMAs per slot,
+        //   K operands read two slots ahead;
+        // - the vector ALU turns S(i) into unnormalised probabilities
+        //   p = exp2(s c - m c), rounded to f16 (RNE) into the P^T operands,
+        //   four values per lane and slot: P^T block kk (cells 16 kk ..
+        //   16 kk + 15, registers 8 (kk & 1) .. + 7 of S^T block kk / 2) is
+        //   complete after slot 2 kk + 1;
+        // - O^T += V(i)^T P(i)^T for block kk in slots 2 kk + 2 (dims blocks
+        //   0, 1) and 2 kk + 3 (2, 3), with the f16 probabilities' row sums,
+        //   V operands read one slot ahead; block 3 in the tail, beside the
+        //   lane maxima of S(i + 1).
+        // So every slot from the third on keeps the matrix cores busy with
+        // four MFMAs while the vector ALU computes its exponentials (phases
+        // of exponentials and of P V products one after the other left the
+        // MFMAs of the second idle behind the first's vector work). The
+        // products accumulate in the same order as block by block.
         float mx;                                 // lane max of S(i + 1), from body(i) (fast mode)
         auto body = [&](const int i, const bool qk, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
             const float mc = m_run == -AL_INF ? 0.0f : m_run * cexp;
@@ -561,9 +568,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             // keeps every buffer's read addresses live across the loop
             int kb_ = kbuf(i + 1), vb_ = vbuf(i);
             asm volatile("" : "+s"(kb_), "+s"(vb_));
+            const half2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
             half8 pf[4];
             half8 kq[8][2];
-            half8 vc[4], vn[4];
+            half8 vn[2], vc[2], v3[4];
             if (qk) {
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
@@ -579,9 +587,14 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                     kq[ks + 2][0] = k_read(kb_, 0, ks + 2);
                     kq[ks + 2][1] = k_read(kb_, 1, ks + 2);
                 }
+                if (ks >= 1 && ks <= 6) {             // the next slot's V operands
+                    const int b = (ks - 1) >> 1, d0 = 2 * ((ks + 1) & 1);
+                    vn[0] = v_read(vb_, b, d0);
+                    vn[1] = v_read(vb_, b, d0 + 1);
+                }
                 if (ks == 7) {
 #pragma unroll
-                    for (int db = 0; db < 4; ++db) vc[db] = v_read(vb_, 0, db);
+                    for (int db = 0; db < 4; ++db) v3[db] = v_read(vb_, 3, db);
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 const int cb = ks >> 2, v0 = 4 * (ks & 3), kk = 2 * cb + (v0 >> 3), e0 = v0 & 4;
@@ -598,41 +611,40 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                     nxt[0] = mfma32(kq[ks][0], qf[ks], nxt[0]);
                     nxt[1] = mfma32(kq[ks][1], qf[ks], nxt[1]);
                 }
+                if (ks >= 2) {                        // O^T += V^T P^T, block (ks - 2) / 2, two dims blocks
+                    const int b = (ks - 2) >> 1, d0 = 2 * (ks & 1);
+#pragma unroll
+                    for (int w = d0; w < d0 + 2; ++w)
+                        l_run = __builtin_amdgcn_fdot2(half2v{pf[b][2 * w], pf[b][2 * w + 1]}, one2, l_run, false);
+                    o[d0] = mfma32(vc[0], pf[b], o[d0]);
+                    o[d0 + 1] = mfma32(vc[1], pf[b], o[d0 + 1]);
+                }
+                vc[0] = vn[0];
+                vc[1] = vn[1];
                 __builtin_amdgcn_sched_barrier(0);
             }
-            // fast mode: S(i + 1) prepared here and its lane max taken in the
-            // slots of phase B (from slot 1 on, when the last QK^T results
-            // are ready); general mode prepares it after the body
+            // tail: block 3's products and row sums; S(i + 1) prepared and its
+            // lane maxima taken (fast mode; general mode prepares it after the
+            // body) while they run
+#pragma unroll
+            for (int w = 0; w < 4; ++w)
+                l_run = __builtin_amdgcn_fdot2(half2v{pf[3][2 * w], pf[3][2 * w + 1]}, one2, l_run, false);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] = mfma32(v3[db], pf[3], o[db]);
+            __builtin_amdgcn_sched_barrier(0);
             constexpr bool fold = !GEN;
-            if (fold && qk) prepare(nxt, tile_c0(i + 1));
             float mx0 = -AL_INF, mx1 = -AL_INF;
-            const half2v one2 = {(_Float16) 1.0f, (_Float16) 1.0f};
+            if (fold && qk) {
+                prepare(nxt, tile_c0(i + 1));
+                float m0 = fmaxf(fmaxf(nxt[0][0], nxt[0][1]), nxt[0][2]);
+                float m1 = fmaxf(fmaxf(nxt[1][0], nxt[1][1]), nxt[1][2]);
 #pragma unroll
-            for (int kk = 0; kk < 4; ++kk) {
-                if (kk < 3) {
-#pragma unroll
-                    for (int db = 0; db < 4; ++db) vn[db] = v_read(vb_, kk + 1, db);
+                for (int v = 3; v < 15; v += 2) {
+                    m0 = fmaxf(fmaxf(m0, nxt[0][v]), nxt[0][v + 1]);
+                    m1 = fmaxf(fmaxf(m1, nxt[1][v]), nxt[1][v + 1]);
                 }
-                if (fold && qk && kk > 0 && kk < 3) {     // slot 1: block 0, slot 2: block 1
-                    const floatx16 & x = nxt[kk - 1];
-                    float m = fmaxf(fmaxf(x[0], x[1]), x[2]);
-#pragma unroll
-                    for (int v = 3; v < 15; v += 2) m = fmaxf(fmaxf(m, x[v]), x[v + 1]);
-                    m = fmaxf(m, x[15]);
-                    if (kk == 1) mx0 = m;
-                    else mx1 = m;
-                }
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    l_run = __builtin_amdgcn_fdot2(half2v{pf[kk][2 * w], pf[kk][2 * w + 1]}, one2, l_run, false);
-#pragma unroll
-                for (int db = 0; db < 4; ++db) o[db] = mfma32(vc[db], pf[kk], o[db]);
-                if (kk < 3) {
-#pragma unroll
-                    for (int db = 0; db < 4; ++db) vc[db] = vn[db];
-                }
-                __builtin_amdgcn_sched_barrier(0);
+                mx0 = fmaxf(m0, nxt[0][15]);
+                mx1 = fmaxf(m1, nxt[1][15]);
             }
             mx = fmaxf(mx0, mx1);
         };
