@@ -33,9 +33,12 @@
 // cores while the vector ALU turns the scores of tile i into probabilities,
 // then PV of tile i; the slots of both phases are ordered explicitly (LDS
 // reads prefetched one or two slots ahead, exponentials pinned to their
-// slot), so the two units overlap within each wave. Softmax: the running
-// max is kept on raw scores (scale > 0 keeps their order), p = exp2(s c -
-// m c) with c = scale log2(e), row sums accumulate by v_dot2 of the f16 P
+// slot), so the two units overlap within each wave. Softmax: p = exp2(s c -
+// b) with c = scale log2(e) and b the row's reference max in log2 units;
+// without softcap the fast loop has the MFMAs produce s c - b directly (the
+// query rows scaled by c before their f16 rounding, the score accumulators
+// started from -b), with softcap or a general mask p = exp2(s' c - m c)
+// from the scores as they are. Row sums accumulate by v_dot2 of the f16 P
 // with ones, and the reference max moves lazily (only when a tile exceeds
 // it by more than kTau in natural units) on a cold path outside the fast
 // loop, so the O accumulators stay in the matrix cores' registers there.
@@ -370,13 +373,29 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
 
     // ---- computing waves ----
     const float cexp = SOFTCAP ? kLog2e : p.scale * kLog2e;
-    const float tau = kTau * kLog2e / cexp;               // kTau in units of s
     floatx16 o[4];
+    // m_run in state units: log2 units (s c) in folded mode, else the units
+    // of the scores the loop keeps (s, or the softcapped s')
     float m_run = -AL_INF, l_run = 0.0f;
     // The computing waves' work, compiled twice: GEN = the general-mask
     // mode, so that its per-value mask reads cost the fast loop nothing.
     auto compute = [&](auto gen_tag) {
         constexpr bool GEN = decltype(gen_tag)::value;
+        // Folded mode (fast mode without softcap) keeps each score as t =
+        // s c - b, b the row's reference max in log2 units (0 until the row
+        // has one): the query rows are scaled by c before their f16 rounding
+        // and the score MFMAs start from -b instead of 0, so p = exp2(t)
+        // takes the scores as they are. Otherwise p = exp2(s c - m c).
+        constexpr bool FOLD = !SOFTCAP && !GEN;
+        const float cu = FOLD ? 1.0f : cexp;             // state units -> log2 units
+        const float tau = kTau * kLog2e / cu;            // kTau in state units
+        floatx16 negb = {};                               // -b in every register (folded mode)
+        // the row's last visible cell less 4 h: cell c0 + 4 h + off is
+        // visible when off <= limh - c0 (padding rows of a ragged last tile:
+        // none in general mode, so that they read no mask values; in fast
+        // mode they keep the INT32_MAX limit)
+        const int limh = (GEN && !rvalid ? -1 : lim) - 4 * h;
+        float thr = -AL_INF;                              // folded mode: rescale when some t exceeds it
         // general mode: this lane's mask row and the factor of its values
         // (ALiBi slope, arm.cpp:2294, over the scale the scores lack)
         const _Float16 * mrow = nullptr;
@@ -419,6 +438,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             if (!kShareQ || si == 0) {
 #pragma unroll
                 for (int ks = 0; ks < 8; ++ks) {
+                    if constexpr (FOLD) {
+                        qv[2 * ks] *= cexp;
+                        qv[2 * ks + 1] *= cexp;
+                    }
                     qf[ks] = rvalid ? to_half8(qv[2 * ks], qv[2 * ks + 1]) : half8{0, 0, 0, 0, 0, 0, 0, 0};
                     if (kShareQ) *(half8 *) (qshare + qslot(ks)) = qf[ks];
                 }
@@ -457,16 +480,30 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             }
             return fmaxf(fmaxf(m0, sc[0][15]), fmaxf(m1, sc[1][15]));
         };
-        auto rescale = [&](const floatx16 (&sc)[2]) {   // move the reference max of outgrown rows
-            const float mt = pair_max(lane_max(sc));
+        auto rescale = [&](floatx16 (&sc)[2]) {         // move the reference max of outgrown rows
+            const float base = FOLD ? -negb[0] : 0.0f;
+            const float mt = pair_max(lane_max(sc)) + base;
             const bool g = mt > m_run + tau;
             const float mn = g ? mt : m_run;
-            const float alpha = g ? __builtin_amdgcn_exp2f((m_run - mn) * cexp) : 1.0f;   // 0 from -inf
+            const float alpha = g ? __builtin_amdgcn_exp2f((m_run - mn) * cu) : 1.0f;   // 0 from -inf
 #pragma unroll
             for (int db = 0; db < 4; ++db) o[db] *= alpha;
             l_run *= alpha;
             m_run = mn;
+            if constexpr (FOLD) {                     // the new base: scores and MFMA start follow
+                const float nb = mn == -AL_INF ? 0.0f : mn;
+                const float sh = nb - base;
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) sc[cb][v] -= sh;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) negb[v] = -nb;
+                thr = mn == -AL_INF ? -AL_INF : tau;
+            }
         };
+        // some score of the tile above the rescale threshold (lane maximum mx)
+        auto outgrows = [&](const float mx) { return FOLD ? mx > thr : mx > m_run + tau; };
         // fresh scores: softcap, -inf for cells of a tile that some row of
         // the wave does not wholly see, and the reference max moved when the
         // tile outgrows it (a rare, uniform branch; the first visible tile
@@ -495,7 +532,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 // (cell c0 + 4 h + off visible when off <= d; the offsets
                 // are immediates of the compares and loads; padding rows of
                 // a ragged last tile load nothing)
-                const int d = (rvalid ? lim : -1) - c0 - 4 * h;
+                const int d = limh - c0;
                 const _Float16 * mt = mrow + c0 + 4 * h;
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
@@ -513,13 +550,16 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             } else if (c0 + kTC - 1 > lim_min) {
                 // cell c0 + 4 h + off is visible when off <= d: one register
                 // per tile, the offsets are immediates
-                const int d = lim - c0 - 4 * h;
+                // (-inf from a scalar register: no vector register held for it)
+                const int d = limh - c0;
+                float ninf = -AL_INF;
+                asm volatile("" : "+s"(ninf));
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                     for (int v = 0; v < 16; ++v) {
                         const int off = 32 * cb + (v & 3) + 8 * (v >> 2);
-                        sc[cb][v] = off <= d ? sc[cb][v] : -AL_INF;
+                        sc[cb][v] = off <= d ? sc[cb][v] : ninf;
                     }
             }
         };
@@ -527,7 +567,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // it (a rare, uniform branch; the first visible tile always does)
         auto finish_scores = [&](floatx16 (&sc)[2], const int c0) {
             prepare(sc, c0);
-            if (__any(lane_max(sc) > m_run + tau)) rescale(sc);
+            if (__any(outgrows(lane_max(sc)))) rescale(sc);
         };
         auto k_read = [&](const int kbo, const int cb, const int ks) {
             const int c = 32 * cb + lr;
@@ -563,7 +603,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         // products accumulate in the same order as block by block.
         float mx;                                 // lane max of S(i + 1), from body(i) (fast mode)
         auto body = [&](const int i, const bool qk, floatx16 (&cur)[2], floatx16 (&nxt)[2]) {
-            const float mc = m_run == -AL_INF ? 0.0f : m_run * cexp;
+            const float mc = FOLD || m_run == -AL_INF ? 0.0f : m_run * cexp;
             // the buffers' offsets as opaque values: otherwise the compiler
             // keeps every buffer's read addresses live across the loop
             int kb_ = kbuf(i + 1), vb_ = vbuf(i);
@@ -578,8 +618,8 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                     kq[ks][0] = k_read(kb_, 0, ks);
                     kq[ks][1] = k_read(kb_, 1, ks);
                 }
-                nxt[0] = floatx16{};
-                nxt[1] = floatx16{};
+                nxt[0] = FOLD ? negb : floatx16{};
+                nxt[1] = FOLD ? negb : floatx16{};
             }
 #pragma unroll
             for (int ks = 0; ks < 8; ++ks) {
@@ -600,8 +640,10 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 const int cb = ks >> 2, v0 = 4 * (ks & 3), kk = 2 * cb + (v0 >> 3), e0 = v0 & 4;
 #pragma unroll
                 for (int u = 0; u < 4; u += 2) {
-                    const float2v e = {__builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u], cexp, -mc)),
-                                      __builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u + 1], cexp, -mc))};
+                    const float2v e = FOLD ? float2v{__builtin_amdgcn_exp2f(cur[cb][v0 + u]),
+                                                     __builtin_amdgcn_exp2f(cur[cb][v0 + u + 1])}
+                                           : float2v{__builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u], cexp, -mc)),
+                                                     __builtin_amdgcn_exp2f(__builtin_fmaf(cur[cb][v0 + u + 1], cexp, -mc))};
                     half2v hv = __builtin_convertvector(e, half2v);
                     asm volatile("" : "+v"(hv));          // keeps the exponentials in this slot
                     pf[kk][e0 + u] = hv[0];
@@ -671,7 +713,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
                 __syncthreads();                  // (B_i) K(i + 1), V(i) landed; iteration i - 1 done
                 body(i, true, cur, nxt);
                 if constexpr (GEN) finish_scores(nxt, tile_c0(i + 1));
-                else if (__any(mx > m_run + tau)) rescale(nxt);
+                else if (__any(outgrows(mx))) rescale(nxt);
             };
             int i = 0;
             for (; i + 2 < NI; i += 2) {
@@ -697,12 +739,14 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         if (MASK && general) compute(std::bool_constant<MASK>{});
         else compute(std::false_type{});
     }
-    float m_nat = m_run == -AL_INF ? -AL_INF : m_run * (cexp / kLog2e);
+    const float cu_run = !SOFTCAP && !(MASK && general) ? 1.0f : cexp;   // m_run's units -> log2 units
+    float m_nat = m_run == -AL_INF ? -AL_INF : m_run * (cu_run / kLog2e);
     float l_row = pair_sum(l_run);
-    // The epilogue's row (an opaque copy: its LDS offsets are computed here,
-    // not hoisted above the loop and held in registers across it)
-    int rre = rr;
-    asm volatile("" : "+v"(rre));
+    // The epilogue's lane, row and half read anew: their LDS offsets are
+    // computed here, not held in registers across the loop.
+    const int lane_e = lane_id_fresh();
+    const int he = lane_e >> 5;
+    const int rre = 32 * rg + (lane_e & 31);
 
     // One workgroup per row tile and two cell splits in it: both splits put
     // their rows' states into LDS records [split][row][132] at once, then
@@ -717,9 +761,9 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq)
-                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * h) =
+                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * he) =
                         float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
-            if (h == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
+            if (he == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
         }
         __syncthreads();
         for (int item = threadIdx.x; item < rows_here * 32; item += 2 * kWaves * 64) {
@@ -752,9 +796,9 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq)
-                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * h) =
+                    *(float4 *) (rec + 32 * db + 8 * bq + 4 * he) =
                         float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
-            if (h == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
+            if (he == 0) *(float2 *) (rec + 128) = float2{m_nat, l_row};
         }
         __syncthreads();
     }
@@ -769,7 +813,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
         for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int bq = 0; bq < 4; ++bq) {
-                const float4 x = *(const float4 *) (rec + 32 * db + 8 * bq + 4 * h);
+                const float4 x = *(const float4 *) (rec + 32 * db + 8 * bq + 4 * he);
                 o[db][4 * bq] = o[db][4 * bq] * wa + x.x * wb;
                 o[db][4 * bq + 1] = o[db][4 * bq + 1] * wa + x.y * wb;
                 o[db][4 * bq + 2] = o[db][4 * bq + 2] * wa + x.z * wb;
@@ -794,7 +838,7 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq) {
-                    const int g = 8 * db + 2 * bq + h;
+                    const int g = 8 * db + 2 * bq + he;
                     *(float4 *) (stage + rre * 128 + 4 * (g ^ (rre & 31))) =
                         apply_scale(float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]}, rs);
                 }
@@ -831,11 +875,11 @@ __global__ __launch_bounds__(2 * kWaves * 64) void fattn_prefill_kernel(const Fa
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int bq = 0; bq < 4; ++bq) {
-                    const int g = 8 * db + 2 * bq + h;
+                    const int g = 8 * db + 2 * bq + he;
                     *(float4 *) (stage + rre * 128 + 4 * (g ^ (rre & 31))) =
                         float4{o[db][4 * bq], o[db][4 * bq + 1], o[db][4 * bq + 2], o[db][4 * bq + 3]};
                 }
-            if (h == 0) ml_stage[rre] = float2{m_nat, l_row};
+            if (he == 0) ml_stage[rre] = float2{m_nat, l_row};
         }
         __syncthreads();
         for (int i = threadIdx.x; i < rows_here * kGran; i += 2 * kWaves * 64) {

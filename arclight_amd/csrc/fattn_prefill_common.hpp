@@ -32,6 +32,15 @@ __device__ __forceinline__ float pair_sum(float x) {
     return __builtin_bit_cast(float, (int) r[0]) + __builtin_bit_cast(float, (int) r[1]);
 }
 
+// The lane's index within the wave read anew by v_mbcnt behind an opaque
+// asm statement: code after a long loop derives its lane-dependent offsets
+// from it instead of holding them in registers across the loop.
+__device__ __forceinline__ int lane_id_fresh() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 // tanh(x / c2 * 2 log2 e) = 1 - 2 / (2^(c2 x) + 1), with the hardware exp2
 // and reciprocal: an absolute error of a few 1e-7 (and -1 / +1 exactly where
 // 2^(c2 x) underflows to 0 or overflows to inf) in four instructions and no

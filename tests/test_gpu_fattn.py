@@ -300,6 +300,27 @@ def test_prefill_kernel_explicit_masks_ragged_tiles(gpu):
         _check(f"prefill T={T} G={Hq // 8}, ragged last tile, mask with holes", q, k, v, mh, scale=SCALE)
 
 
+def test_prefill_kernel_scores_outgrow_the_reference(gpu):
+    # Scores that climb by several times the lazy-rescale threshold (8
+    # natural units) from tile to tile for some rows, so the reference max
+    # moves inside the loop, with the scores of the next tile already
+    # computed against the old one; other rows fall, keeping the first
+    # tile's. Dimension 0 carries the ramp: s += a * 0.25 c (cell c), a per
+    # row in {-3, -1, 0, 2, 4, 6}: 1.4 a natural units per 64-cell tile.
+    rng = np.random.default_rng(2201)
+    for seed, T, Hq, n_kv, pos0 in ((2202, 256, 32, 1024, 768), (2203, 512, 64, 1536, 1024)):
+        q, k, v = O.make_inputs(seed, T=T, Hq=Hq, Hkv=8, n_kv=n_kv)
+        q[..., 0] = rng.choice(np.array([-3.0, -1.0, 0.0, 2.0, 4.0, 6.0], dtype=np.float32), size=q.shape[:-1])
+        k[..., 0] = (0.25 * np.arange(n_kv)).astype(np.float16)[None, :, None]
+        name = f"prefill T={T} Hq={Hq}, growing scores"
+        _check(f"{name}, length / causal rule", q, k, v, scale=SCALE, kv_len=pos0 + T, causal_pos0=pos0)
+        m = O.causal_mask(T, n_kv, pos0, kv_len=pos0 + T)
+        _check(f"{name}, prefix mask", q, k, v, m, scale=SCALE)
+        mh = m.copy()
+        mh[0, 0, 3:T - 5, 40:70] = -np.inf                                # holes: the general mode
+        _check(f"{name}, mask with holes", q, k, v, mh, scale=SCALE)
+
+
 def test_prefill_kernel_streams_ragged(gpu):
     # two streams, rows not a multiple of 64, cells not a multiple of 32
     q, k, v = O.make_inputs(601, B=2, T=510, Hq=16, Hkv=4, n_kv=1111)
