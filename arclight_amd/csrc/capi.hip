@@ -300,6 +300,13 @@ int decode_merge_rows() {
     static int v = env_int("AL_DECODE_MERGE_ROWS", 8);
     return v;
 }
+// AL_DECODE_MASK_PRE=0: decode loads the mask rows with every stage, never
+// preloaded (read on every call that has a mask tensor, so that one process
+// can compare the two forms).
+bool decode_mask_pre() {
+    const char * s = getenv("AL_DECODE_MASK_PRE");
+    return !(s && s[0] == '0');
+}
 // Most splits per (stream, kv head) (AL_DECODE_MAX_SPLIT, at most kFattnMaxSplit).
 int decode_max_split() {
     static int v = std::min(env_int("AL_DECODE_MAX_SPLIT", kFattnMaxSplit), kFattnMaxSplit);
@@ -459,7 +466,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         dwaves = 8;
         stages = 2;
     }
-    const size_t decode_lds = fattn_decode_lds_bytes(dwaves, stages, m.data != nullptr);
+    const size_t decode_lds = fattn_decode_lds_bytes(dwaves, stages, m.data != nullptr, false);
     const bool mask_ok = !m.data || (p.m_slice_bytes < INT32_MAX && aligned16(m.data) && m.nb[1] % 16 == 0 &&
                                      m.nb[2] % 16 == 0 && m.nb[3] % 16 == 0);
     const int64_t decode_units = Hkv * B;
@@ -493,6 +500,24 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.n_split = (int32_t) ((nst + cps - 1) / cps);
         p.interleave = decode_interleave() ? 1 : 0;
         p.merge_rows = decode_merge_rows();
+        // A mask tensor: each wave's mask values go into LDS before its first
+        // stage when the workgroup's share fits kDecodeMaskPreBytes (32 bytes
+        // per stage and distinct mask row: the tokens when the heads share
+        // the mask rows, else the query rows; AL_DECODE_MASK_PRE=0: with
+        // every stage instead)
+        if (m.data && decode_mask_pre()) {
+            const int64_t rows_here = std::min<int64_t>(pl.rows_per_tile, p.R);
+            const int64_t D = m.ne[2] == 1 ? (rows_here - 1) / p.G + 1 : rows_here;
+            const int64_t per_wave = p.interleave ? (nst + (int64_t) dwaves * p.n_split - 1) / ((int64_t) dwaves * p.n_split)
+                                                  : (cps + dwaves - 1) / dwaves;
+            const int64_t wave_bytes = (per_wave * D + 31) / 32 * 1024;
+            if (wave_bytes * dwaves <= kDecodeMaskPreBytes &&
+                (size_t) lds_per_block >= fattn_decode_lds_bytes(dwaves, stages, true, true) + decode_q_lds) {
+                p.mask_pre = 1;
+                p.mask_rows = (int32_t) D;
+                p.mask_wave_bytes = (int32_t) wave_bytes;
+            }
+        }
         if (p.n_split > 1) {
             pl.part_offset = kFattnCounterBytes;
             pl.part_bytes = (size_t) decode_units * p.n_split * pl.rows_per_tile * kDecodeRecRow;

@@ -71,18 +71,22 @@ __device__ __forceinline__ float max32(float x) {
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 // FM < 0: the query rows come ready in p.q; FM >= 0: the attention inputs
-// folded in (DecodeInputs), FM the rotation mode.
-template <int WS, int NB, bool HAS_MASK, int RB, int FM>
+// folded in (DecodeInputs), FM the rotation mode. MASK: 0 no mask tensor, 1
+// its rows loaded with every stage, 2 the mask values of all of a wave's
+// stages preloaded into LDS before its first stage (p.mask_pre).
+template <int WS, int NB, int MASK, int RB, int FM>
 __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p, const DecodeInputs in) {
     constexpr bool FUSED = FM >= 0;
+    constexpr bool HAS_MASK = MASK != 0;
     static_assert(WS == 2 || WS == 4 || WS == 8, "the wave merge is a binary tree");
     static_assert(RB == 1 || RB == 2, "16 or 32 rows");
-    constexpr int PER = 8 + (HAS_MASK ? 1 : 0);           // DMA loads per stage
-    constexpr int STAGE = 8192 + (HAS_MASK ? 1024 : 0);   // K rows, V rows, mask rows
+    constexpr int PER = 8 + (MASK == 1 ? 1 : 0);          // DMA loads per stage
+    constexpr int STAGE = 8192 + (MASK == 1 ? 1024 : 0);  // K rows, V rows, mask rows
     constexpr int REC = 16 * RB * kRowStride;             // floats of one state record (16 RB rows)
     static_assert(WS * NB * STAGE >= (WS / 2 > 0 ? WS / 2 : 1) * REC * 4, "LDS merge records must fit the rings");
     __shared__ __attribute__((aligned(1024))) char lds[WS][NB][STAGE];
     __shared__ __attribute__((aligned(1024))) char qlds[16 * RB * 512];  // the query rows, f32
+    __shared__ __attribute__((aligned(1024))) char mpre[MASK == 2 ? kDecodeMaskPreBytes : 16];
     // fused inputs: 1 KiB slots of q_w, k_w and the new token's k and v rows
     // for this kv head (512 bytes each), then the new K (normed, rotated) and
     // V rows as f16 (256 bytes each) and the rotation pairs' (cos, sin)
@@ -128,7 +132,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         const int c_e = range_end(h);
         return c_e > wbase ? (c_e - wbase + wstride - 1) / wstride : 0;
     };
-    const int n_pre = min(NB - 1, wave_stages(p.dyn ? p.kv_hi : limit(p.kv_hi, p.causal_pos0)));  // issued ahead
+    const int ns_bound = wave_stages(p.dyn ? p.kv_hi : limit(p.kv_hi, p.causal_pos0));  // at the launch's bound
+    const int n_pre = min(NB - 1, ns_bound);                          // issued ahead
 
     // K/V rows of this stream and head (loads past the end read 0)
     const uint32_t k_nb1 = (uint32_t) p.k_nb1, v_nb1 = (uint32_t) p.v_nb1;
@@ -160,15 +165,16 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         head[rb] = kvh * p.G + (rvalid[rb] ? r - t * p.G : 0);
     }
 
-    // Mask rows (f16, cells along a row) also travel by DMA, one 1 KiB block
-    // per stage: lane l loads cells 8(l & 1)..+7 of row l >> 1 to LDS bytes
-    // 16 l (with one row block, lanes 32..63 repeat lanes 0..31), from a
-    // buffer over the stream's mask slice; cells past a row read whatever
-    // follows, and are past the length limit anyway.
+    // Mask rows (f16, cells along a row) also travel by DMA, from a buffer
+    // over the stream's mask slice; cells past a row read whatever follows,
+    // and are past the length limit anyway. MASK 1: one 1 KiB block per
+    // stage, lane l loading cells 8(l & 1)..+7 of row l >> 1 to LDS bytes 16
+    // l (with one row block, lanes 32..63 repeat lanes 0..31). MASK 2: see
+    // the preload below.
     int4v md = {0, 0, 0, 0};
     uint32_t msrc = 0;
-    if constexpr (HAS_MASK) {
-        md = raw_desc(p.mask + (int64_t) (b % p.m_ne3) * p.m_nb3, p.m_slice_bytes);
+    if constexpr (HAS_MASK) md = raw_desc(p.mask + (int64_t) (b % p.m_ne3) * p.m_nb3, p.m_slice_bytes);
+    if constexpr (MASK == 1) {
         const int mrow = (lane >> 1) & (16 * RB - 1);
         const int mr = mrow < rows_here ? mrow : 0;
         const int mt_ = div_g(mr, p.G, p.g_magic);
@@ -186,7 +192,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
             dma16(kd, kofs + (uint32_t) (4 * i) * k_nb1 + dj[i], base + (uint32_t) (i * 1024));
             dma16(vd, vofs + (uint32_t) (4 * i) * v_nb1 + dj[i], base + (uint32_t) (4096 + i * 1024));
         }
-        if constexpr (HAS_MASK) dma16(md, msrc + cs * 2, base + 8192u);
+        if constexpr (MASK == 1) dma16(md, msrc + cs * 2, base + 8192u);
     };
 
     // The query rows travel by LDS-DMA too, ahead of the first stages, so
@@ -232,6 +238,31 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         const uint32_t * rw = (const uint32_t *) in.rows;
         const uint32_t rlo = ld_uniform(rw), rhi = ld_uniform(rw + (in.rows64 ? 1 : 0));
         row_0 = in.rows64 ? (int64_t) (((uint64_t) rhi << 32) | rlo) : (int64_t) (int32_t) rlo;
+    }
+    // MASK 2: the mask values of this wave's stages (at the launch's bound)
+    // into its LDS region, 32 bytes per (stage j, distinct mask row d) at
+    // item j * D + d, before the first stages, so every wait for a stage
+    // also covers them: DMA block k holds items 32 k .. 32 k + 31, lanes 2i
+    // and 2i + 1 the two halves of item 32 k + i. D = p.mask_rows: the
+    // workgroup's tokens when the mask rows are shared by the heads
+    // (m_ne2 = 1), else its query rows. Items past the wave's last stage read
+    // past the mask slice (zeros).
+    if constexpr (MASK == 2) {
+        const int D = p.mask_rows;
+        const int items = ns_bound * D;
+        const uint32_t mbase = lds_addr(mpre) + (uint32_t) (ws * p.mask_wave_bytes);
+        for (int k = 0; 32 * k < items; ++k) {
+            const int i = 32 * k + (lane >> 1);
+            const int j = i / D, d = i - j * D;
+            uint32_t off = 0xfffffff0u;
+            if (i < items) {
+                const int t = p.m_ne2 == 1 ? d : div_g(d, p.G, p.g_magic);
+                const int hm = p.m_ne2 == 1 ? 0 : (kvh * p.G + d - t * p.G) % p.m_ne2;
+                off = (uint32_t) ((int64_t) t * p.m_nb1 + (int64_t) hm * p.m_nb2) +
+                      (uint32_t) (wbase + wstride * j) * 2u + (uint32_t) ((lane & 1) * 16);
+            }
+            dma16(md, off, mbase + (uint32_t) (k * 1024));
+        }
     }
 #pragma unroll
     for (int u = 0; u < NB - 1; ++u)
@@ -397,6 +428,15 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         l_run[rb] = 0.0f;
     }
 
+    // MASK 2: this lane's items in the wave's preloaded mask values (row
+    // block rb: cells 4g .. 4g + 3 of its distinct mask row), per stage + 32 D
+    const char * mp[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+        const int d = p.m_ne2 == 1 ? tok[rb] : (rvalid[rb] ? 16 * rb + n : 0);
+        mp[rb] = mpre + ws * p.mask_wave_bytes + d * 32 + 8 * g;
+    }
+
     // LDS read offsets of this lane within a stage
     const int kread = n * 256;                                          // K row of cell n
     const int vcell = 4 * g + (n >> 2);                                 // V cell this lane supplies
@@ -434,7 +474,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 mk[rb] = uint2{0, 0};
-                if constexpr (HAS_MASK) mk[rb] = *(const uint2 *) (st + 8192 + 32 * (16 * rb + n) + 8 * g);
+                if constexpr (MASK == 1) mk[rb] = *(const uint2 *) (st + 8192 + 32 * (16 * rb + n) + 8 * g);
+                if constexpr (MASK == 2) mk[rb] = *(const uint2 *) (mp[rb] + j * 32 * p.mask_rows);
             }
 
             // a stage is taken whole when the length / causal limit passes it
@@ -782,8 +823,9 @@ template <int WS, int NB>
 hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
     const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
     const DecodeInputs none = {};
-    if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, true, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
-    else        hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 2, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 1, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    else                      hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
     return hipGetLastError();
 }
 
@@ -791,9 +833,9 @@ template <int WS, int NB>
 hipError_t launch_fused(const FattnParams & p, const DecodeInputs & in, const int mode, hipStream_t stream) {
     const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, 1);
     switch (mode) {
-        case 2: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 2>), grid, dim3(WS * 64), 0, stream, p, in); break;
-        case 1: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 1>), grid, dim3(WS * 64), 0, stream, p, in); break;
-        default: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, false, 1, 0>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        case 2: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 2>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        case 1: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 1>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        default: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 0>), grid, dim3(WS * 64), 0, stream, p, in); break;
     }
     return hipGetLastError();
 }
@@ -807,8 +849,8 @@ bool fattn_decode_config_ok(int waves, int stages) {
     }
 }
 
-size_t fattn_decode_lds_bytes(int waves, int stages, bool mask) {
-    return (size_t) waves * stages * (8192 + (mask ? 1024 : 0));
+size_t fattn_decode_lds_bytes(int waves, int stages, bool mask, bool mask_pre) {
+    return (size_t) waves * stages * (8192 + (mask && !mask_pre ? 1024 : 0)) + (mask && mask_pre ? kDecodeMaskPreBytes : 0);
 }
 
 hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream) {
@@ -817,8 +859,9 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
         if (p.R > 32 || waves != 8 || stages != 2) return hipErrorInvalidValue;
         const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
         const DecodeInputs none = {};
-        if (p.mask) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, true, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
-        else        hipLaunchKernelGGL((fattn_decode_kernel<8, 2, false, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
+        if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 2, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
+        else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 1, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
+        else                      hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 0, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
         return hipGetLastError();
     }
     switch (waves * 10 + stages) {

@@ -37,6 +37,9 @@ struct FattnParams {
     int32_t cells_per_split;        // multiple of 32
     int32_t interleave;             // decode kernel: splits take every n_split-th 16-cell stage
     int32_t merge_rows;             // decode kernel: query rows per merging workgroup
+    int32_t mask_pre;               // decode kernel: each wave's mask values preloaded into LDS
+    int32_t mask_rows;              //   distinct mask rows of a workgroup (32-byte items per stage)
+    int32_t mask_wave_bytes;        //   LDS bytes per wave (whole 1 KiB DMA blocks)
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
     int *      err;                 // device error flags (al_device_errors): [0, 1] set_rows, [2] a merge gave up waiting
@@ -102,7 +105,9 @@ bool fattn_decode_fused_ok(int waves, int stages);
 int attn_inputs_decode(const struct al_attn_inputs_args * a, DecodeInputs * out, int * mode);
 hipError_t fattn_decode_launch_fused(const FattnParams & p, const DecodeInputs & in, int mode, int waves, int stages,
                                      hipStream_t stream);
-size_t fattn_decode_lds_bytes(int waves, int stages, bool mask);
+size_t fattn_decode_lds_bytes(int waves, int stages, bool mask, bool mask_pre);
+// LDS for the preloaded mask values of a decode workgroup (all its waves).
+constexpr int kDecodeMaskPreBytes = 16384;
 hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hipStream_t stream);
 
 // Floats of one split-KV merge record row (O[128], m, l, pad).

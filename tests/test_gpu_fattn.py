@@ -372,3 +372,47 @@ def test_decode_kernel_two_row_blocks_explicit_mask(gpu):
     m[..., 200:260] = rng.uniform(-3, 0, (1, 1, m.shape[2], 60)).astype(np.float16)
     m[..., 300] = -np.inf
     _check("two row blocks, mask with biases, ALiBi, 2 streams", q, k, v, m, scale=SCALE, max_bias=8.0)
+
+
+def test_decode_mask_preloaded_and_per_stage(gpu, monkeypatch):
+    """A decode call with a mask tensor loads each wave's mask values into LDS
+    once, before its first stage, when the workgroup's share fits
+    (AL_DECODE_MASK_PRE=0: with every stage instead). Both forms apply the
+    same mask values in the same order, so they give the same bits, and both
+    match the oracle: one token over a mask with holes and finite values
+    shared by the heads, eight drafts with the causal mask among them
+    (32 rows, two row blocks), four drafts with per-head mask planes, and a
+    one-token call whose share is too large to preload (131072 cells, two
+    mask planes that the heads alternate between: both settings take the
+    per-stage form there)."""
+    rng = np.random.default_rng(77)
+    cases = []
+    q, k, v = O.make_inputs(771, T=1, Hq=32, Hkv=8, n_kv=4096)
+    m = np.zeros((1, 1, 64, 4096), np.float16)
+    m[0, 0, 0, rng.choice(4096, 700, replace=False)] = -np.inf
+    m[0, 0, 0, :512] = rng.uniform(-2, 0, 512).astype(np.float16)
+    m[0, 0, 0, 4000:] = -np.inf
+    cases.append(("one token, holes and finite values", q, k, v, m))
+    q, k, v = O.make_inputs(772, T=8, Hq=32, Hkv=8, n_kv=8448)
+    cases.append(("eight drafts, causal", q, k, v, O.causal_mask(8, 8448, 8192, kv_len=8200)))
+    q, k, v = O.make_inputs(773, T=4, Hq=32, Hkv=8, n_kv=2048)
+    mh = rng.uniform(-1, 0, size=(1, 32, 64, 2048)).astype(np.float16)
+    mh[..., 1900:] = -np.inf
+    mh[0, 5, 2, :1000] = -np.inf
+    cases.append(("four drafts, per-head planes", q, k, v, mh))
+    q, k, v = O.make_inputs(774, T=1, Hq=8, Hkv=2, n_kv=131072)
+    mb = np.zeros((1, 2, 64, 131072), np.float16)
+    mb[0, 0, 0, 120000:] = -np.inf
+    mb[0, 1, 0, :70000] = -np.inf
+    cases.append(("one token, two mask planes, 131072 cells", q, k, v, mb))
+    for name, q, k, v, m in cases:
+        ref = O.attention(q, k, v, m, scale=SCALE)
+        _case(f"{name}: preloaded")
+        monkeypatch.delenv("AL_DECODE_MASK_PRE", raising=False)
+        a = run_gpu(q, k, v, m, scale=SCALE)
+        _case(f"{name}: per stage")
+        monkeypatch.setenv("AL_DECODE_MASK_PRE", "0")
+        b = run_gpu(q, k, v, m, scale=SCALE)
+        monkeypatch.delenv("AL_DECODE_MASK_PRE", raising=False)
+        assert np.array_equal(a, b, equal_nan=True), f"{name}: preloaded and per-stage masks differ"
+        assert_parity(a, ref, what=name)
