@@ -291,14 +291,16 @@ int decode_min_stages() {
     return v;
 }
 // Query rows each merging workgroup of a split decode call takes
-// (AL_DECODE_MERGE_ROWS). A merger is bound by the record bytes its CU
-// loads (32 splits x 520 bytes per row), but every merger polls the same
-// flag line, so few of them: 8 rows each (decode 1 merger, 4-draft verify 2,
-// 8-draft verify 4: 21.7 -> 16.7 us per layer at 8K cells; one per row is
-// slower again).
-int decode_merge_rows() {
-    static int v = env_int("AL_DECODE_MERGE_ROWS", 8);
-    return v;
+// (AL_DECODE_MERGE_ROWS overrides). A merger is bound by the record bytes
+// its CU loads (32 splits x 520 bytes per row), but every merger polls the
+// same flag line, so few of them. Up to 8 rows per kv head (one token, the
+// 2-wave shape): 2 rows each (4K decode 10.07 -> 9.62 us per layer, the
+// decode block 34.05 -> 33.53, 32K unchanged); more rows (verify, the 8-wave
+// shape): 8 rows each (4-draft verify 2 mergers, 8-draft 4: 21.7 -> 16.7 us
+// per layer at 8K cells; 2 rows each 15.2 against 14.2 for 4 drafts).
+int decode_merge_rows(int rows) {
+    static int v = env_int("AL_DECODE_MERGE_ROWS", 0);
+    return v > 0 ? v : (rows <= 8 ? 2 : 8);
 }
 // AL_DECODE_MASK_PRE=0: decode loads the mask rows with every stage, never
 // preloaded (read on every call that has a mask tensor, so that one process
@@ -499,7 +501,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.cells_per_split = (int32_t) (cps * 16);
         p.n_split = (int32_t) ((nst + cps - 1) / cps);
         p.interleave = decode_interleave() ? 1 : 0;
-        p.merge_rows = decode_merge_rows();
+        p.merge_rows = decode_merge_rows((int) std::min<int64_t>(p.R, pl.rows_per_tile));
         // A mask tensor: each wave's mask values go into LDS before its first
         // stage when the workgroup's share fits kDecodeMaskPreBytes (32 bytes
         // per stage and distinct mask row: the tokens when the heads share
