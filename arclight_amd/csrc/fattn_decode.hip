@@ -592,9 +592,11 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         }
     }
 
-    // merge the WS waves through LDS records [slot][row][132] (the rings are
-    // free once every wave is past its loop)
-    if constexpr (WS > 1) {
+    // Four or more waves (kOnePass) merge and publish in one pass (below);
+    // two merge through LDS records [slot][row][132] (the rings are free
+    // once every wave is past its loop), then wave 0 publishes.
+    constexpr bool kOnePass = WS >= 4;
+    if constexpr (WS > 1 && !kOnePass) {
         float * recs = (float *) &lds[0][0][0];
 #pragma unroll
         for (int span = WS / 2; span >= 1; span /= 2) {
@@ -634,7 +636,7 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         }
     }
 
-    if (p.n_split == 1) {
+    if (!kOnePass && p.n_split == 1) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
             if (ws == 0 && rvalid[rb]) {
@@ -675,7 +677,70 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     const int K = min(p.n_split, (rows_here + p.merge_rows - 1) / p.merge_rows);
     const int kidx = ((p.n_split - 1 - split - unit % 8) % p.n_split + p.n_split) % p.n_split;
     unsigned epoch = 0;
-    if (ws == 0) {
+    if constexpr (kOnePass) {
+        // Every wave puts its rows' state into its own ring (its DMA has
+        // landed): O rows of 32 granules, granule j of row r at slot j ^ (r &
+        // 31), and the rows' (m, l) pairs after them, or in the query-row
+        // buffer when the ring has no room (the query rows are in registers;
+        // with the inputs folded in the ring always has room). After one
+        // barrier every thread takes (row, 4 dims) items, combines the WS
+        // states in wave order (the merge records' arithmetic) and writes the
+        // row's output (one split) or this split's record, whose (m, l) pair
+        // comes with the item of dims 0..3; once every wave's stores have
+        // completed, wave 0 sets the split's flag.
+        constexpr int kRecO = 16 * RB * 512;
+        constexpr bool kMLinRing = NB * STAGE - kRecO >= 16 * RB * 8;
+        static_assert(NB * STAGE >= kRecO, "a wave's O rows fit its ring");
+        static_assert(kMLinRing || !FUSED, "the folded inputs keep the query rows until the merge");
+        auto rec_o = [&](const int w) { return &lds[w][0][0]; };
+        auto rec_ml = [&](const int w) {
+            return kMLinRing ? (float2 *) (&lds[w][0][0] + kRecO) : (float2 *) qlds + w * 16 * RB;
+        };
+        // (a wave with no stages gets here while another may still be
+        // reading its query fragments from qlds)
+        if constexpr (!kMLinRing) __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+            const int r = 16 * rb + n;
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb)
+                *(float4 *) (rec_o(ws) + (r * 32 + ((4 * mb + g) ^ (r & 31))) * 16) =
+                    float4{o[rb][mb][0], o[rb][mb][1], o[rb][mb][2], o[rb][mb][3]};
+            if (g == 0) rec_ml(ws)[r] = float2{m_run[rb], l_run[rb]};
+        }
+        if (ws == 0 && p.n_split > 1) epoch = ld_agent_u32(flags + 32);
+        __syncthreads();
+        for (int item = threadIdx.x; item < rows_here * 32; item += WS * 64) {
+            const int r = item >> 5, d4 = item & 31;
+            float M = -AL_INF;
+#pragma unroll
+            for (int w = 0; w < WS; ++w) M = fmaxf(M, rec_ml(w)[r].x);
+            const float Mu = (M == -AL_INF) ? 0.0f : M;
+            float L = 0.0f;
+            float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int w = 0; w < WS; ++w) {
+                const float2 ml = rec_ml(w)[r];
+                const float wt = exp_fast(ml.x - Mu);
+                const float4 x = *(const float4 *) (rec_o(w) + (r * 32 + (d4 ^ (r & 31))) * 16);
+                L += wt * ml.y;
+                acc.x += wt * x.x; acc.y += wt * x.y; acc.z += wt * x.z; acc.w += wt * x.w;
+            }
+            if (p.n_split == 1) {
+                const int t = div_g(r, p.G, p.g_magic);
+                const int hq = kvh * p.G + r - t * p.G;
+                float * out = (float *) (p.dst + ((int64_t) (b * p.T + t) * p.Hq + hq) * p.dst_nb1);
+                *(float4 *) (out + 4 * d4) = finalize4(acc, M, L, p.sinks, hq);
+            } else {
+                buf_store16_dev(acc, pr, (uint32_t) split * RS + (uint32_t) (r * 512 + d4 * 16));
+                if (d4 == 0) buf_store8_dev(float2{M, L}, pr, (uint32_t) split * RS + kPairs0 + (uint32_t) (r * 8));
+            }
+        }
+        if (p.n_split == 1) return;
+        complete_wave_memops();
+        __syncthreads();
+        if (ws == 0 && lane == 0) st_agent_u32(flags + split, epoch + 1u);
+    } else if (ws == 0) {
         epoch = ld_agent_u32(flags + 32);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) {
