@@ -31,6 +31,7 @@
 #define _GNU_SOURCE 1
 #include "fattn_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <sched.h>
@@ -191,6 +192,10 @@ static inline float mask_value(const job_t * j, const uint16_t * mp, float slope
 /* one query row, three numerics                                        */
 /* ------------------------------------------------------------------ */
 
+/* f16 -> f32 of 8 values by the F16C conversion (exact, as
+   orc_f16_to_f32; the oracle is built for x86-64-v3, which has F16C). */
+static inline __m256 h8_to_f32(const uint16_t * x) { return _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) x)); }
+
 static void row_o2_o3(const job_t * j, int64_t ir, float * VKQ32, uint16_t * VKQ16, uint16_t * Q_q) {
     const al_fattn_args * a = j->a;
     const int64_t T = j->T, Hq = j->Hq, D = j->D, DV = j->DV;
@@ -215,6 +220,12 @@ static void row_o2_o3(const job_t * j, int64_t ir, float * VKQ32, uint16_t * VKQ
     const int64_t iv3 = iq3 / j->rv3, iv2 = iq2 / j->rv2;
     const float * pq = (const float *) ((const char *) a->q.data + iq1 * a->q.nb[1] + iq2 * a->q.nb[2] + iq3 * a->q.nb[3]);
     for (int64_t d = 0; d < D; ++d) Q_q[d] = orc_f32_to_f16(pq[d]);       /* arm.cpp:2322 */
+    /* the f32 loops below in 8-wide registers when D and DV are multiples of
+       8: the same per-lane products and sums (separate multiply and add, as
+       the scalar form compiles under ISO C) and the same lane reduction */
+    const int vec = (D % 8 == 0) && (DV % 8 == 0) && D <= 1024;
+    float Qf[1024];
+    if (vec) for (int64_t d = 0; d < D; ++d) Qf[d] = orc_f16_to_f32(Q_q[d]);
 
     for (int64_t ic = 0; ic < j->n_kv; ++ic) {
         const float mv = mask_value(j, mp, slope, iq1, ic);
@@ -224,8 +235,14 @@ static void row_o2_o3(const job_t * j, int64_t ir, float * VKQ32, uint16_t * VKQ
         if (!f16acc) {
             /* f32 lanes of width 8, then a pairwise lane reduction */
             float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-            for (int64_t d = 0; d < D; d += 8) {
-                for (int l = 0; l < 8 && d + l < D; ++l) acc[l] += orc_f16_to_f32(kd[d + l]) * orc_f16_to_f32(Q_q[d + l]);
+            if (vec) {
+                __m256 a8 = _mm256_setzero_ps();
+                for (int64_t d = 0; d < D; d += 8) a8 = _mm256_add_ps(a8, _mm256_mul_ps(h8_to_f32(kd + d), _mm256_loadu_ps(Qf + d)));
+                _mm256_storeu_ps(acc, a8);
+            } else {
+                for (int64_t d = 0; d < D; d += 8) {
+                    for (int l = 0; l < 8 && d + l < D; ++l) acc[l] += orc_f16_to_f32(kd[d + l]) * orc_f16_to_f32(Q_q[d + l]);
+                }
             }
             s = ((acc[0] + acc[4]) + (acc[2] + acc[6])) + ((acc[1] + acc[5]) + (acc[3] + acc[7]));
         } else {
@@ -266,6 +283,10 @@ static void row_o2_o3(const job_t * j, int64_t ir, float * VKQ32, uint16_t * VKQ
         if (f16acc) {
             const uint16_t hv = orc_f32_to_f16(vs);                         /* arm.cpp:1735 */
             for (int64_t d = 0; d < DV; ++d) VKQ16[d] = h_fma(VKQ16[d], vd[d], hv);
+        } else if (vec) {
+            const __m256 vs8 = _mm256_set1_ps(vs);
+            for (int64_t d = 0; d < DV; d += 8)                             /* arm.cpp:2385-2386 */
+                _mm256_storeu_ps(VKQ32 + d, _mm256_add_ps(_mm256_loadu_ps(VKQ32 + d), _mm256_mul_ps(h8_to_f32(vd + d), vs8)));
         } else {
             for (int64_t d = 0; d < DV; ++d) VKQ32[d] += orc_f16_to_f32(vd[d]) * vs;   /* arm.cpp:2385-2386 */
         }
