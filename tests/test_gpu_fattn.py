@@ -416,3 +416,19 @@ def test_decode_mask_preloaded_and_per_stage(gpu, monkeypatch):
         monkeypatch.delenv("AL_DECODE_MASK_PRE", raising=False)
         assert np.array_equal(a, b, equal_nan=True), f"{name}: preloaded and per-stage masks differ"
         assert_parity(a, ref, what=name)
+
+
+def test_verify_waves_without_stages_and_one_pass_merge(gpu):
+    """The 8-wave decode shape (17-32 query rows per kv head) merges its
+    waves in one pass from their own LDS rings. Short contexts leave some of
+    the 8 waves with no stage at all (they reach the merge while the others
+    still work), and with one split the pass writes the output rows itself:
+    8 drafts (two row blocks) over 100, 700 and 5000 cells, 5 drafts (20
+    rows, one row block partly valid) over 90 cells, with the causal mask
+    among the drafts, against the oracle."""
+    for seed, T, n_kv in ((881, 8, 100), (882, 8, 700), (883, 8, 5000), (884, 5, 90)):
+        q, k, v = O.make_inputs(seed, T=T, Hq=32, Hkv=8, n_kv=n_kv)
+        kw = dict(kv_len=n_kv, causal_pos0=n_kv - T)
+        _case(f"{T} drafts over {n_kv} cells")
+        got = run_gpu(q, k, v, scale=SCALE, **kw)
+        assert_parity(got, O.attention(q, k, v, scale=SCALE, **kw), what=f"{T} drafts over {n_kv} cells")
