@@ -425,7 +425,7 @@ def cpu_baseline(a):
             O.attention_pinned(q, k, v, scale=scale, kv_len=ctx, cpus=cpus)
             calls += 1
         el = time.perf_counter() - t0
-        if el >= a.cpu_seconds or calls >= 400:
+        if el >= a.cpu_seconds or calls >= 4000:
             break
     per = el / calls
     byts = decode_bytes(ctx, Hq, Hkv, D)
@@ -440,7 +440,7 @@ def cpu_baseline(a):
             O.attention_pinned(qc, k, v, scale=scale, kv_len=chunk * (c + 1), causal_pos0=chunk * c, cpus=cpus)
         reps += 1
         pel = time.perf_counter() - t0
-        if pel >= a.cpu_seconds or reps >= 20:
+        if pel >= a.cpu_seconds or reps >= 200:
             break
     fl = prefill_flops(T_total, chunk, Hq, D)
     where = (f"{len(cpus)} threads pinned one per physical core; host {topo['model']}, "
