@@ -302,6 +302,16 @@ int decode_merge_rows(int rows) {
     static int v = env_int("AL_DECODE_MERGE_ROWS", 0);
     return v > 0 ? v : (rows <= 8 ? 2 : 8);
 }
+// Splits of up to this many cells (AL_DECODE_ONE_PASS_CELLS, 0: never; read
+// on every call, so that one process can compare the two forms) merge the
+// 2 x 3 shape's two waves in one pass with all threads, which shortens the
+// tail of short splits (4K / 8K / 16K decode 9.5 / 11.5 / 16.4 -> 9.1 / 11.2
+// / 16.1 us per layer, 2-draft verify at 8K 12.9 -> 12.5); with 1024 cells
+// per split (32K) the tree merge is faster (25.8 against 26.7 us).
+int decode_one_pass_cells() {
+    const char * s = getenv("AL_DECODE_ONE_PASS_CELLS");
+    return s && s[0] ? atoi(s) : 512;
+}
 // AL_DECODE_MASK_PRE=0: decode loads the mask rows with every stage, never
 // preloaded (read on every call that has a mask tensor, so that one process
 // can compare the two forms).
@@ -502,6 +512,7 @@ int make_plan(const al_fattn_args * a, int n_cu, int lds_per_block, Plan * out) 
         p.n_split = (int32_t) ((nst + cps - 1) / cps);
         p.interleave = decode_interleave() ? 1 : 0;
         p.merge_rows = decode_merge_rows((int) std::min<int64_t>(p.R, pl.rows_per_tile));
+        p.one_pass = dwaves == 2 && stages == 3 && cps * 16 <= decode_one_pass_cells() ? 1 : 0;
         // A mask tensor: each wave's mask values go into LDS before its first
         // stage when the workgroup's share fits kDecodeMaskPreBytes (32 bytes
         // per stage and distinct mask row: the tokens when the heads share

@@ -73,8 +73,10 @@ typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 // FM < 0: the query rows come ready in p.q; FM >= 0: the attention inputs
 // folded in (DecodeInputs), FM the rotation mode. MASK: 0 no mask tensor, 1
 // its rows loaded with every stage, 2 the mask values of all of a wave's
-// stages preloaded into LDS before its first stage (p.mask_pre).
-template <int WS, int NB, int MASK, int RB, int FM>
+// stages preloaded into LDS before its first stage (p.mask_pre). OP: the
+// waves' states merged and the split's record stored in one pass by all
+// threads (always with four or more waves; with two, p.one_pass).
+template <int WS, int NB, int MASK, int RB, int FM, bool OP>
 __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams p, const DecodeInputs in) {
     constexpr bool FUSED = FM >= 0;
     constexpr bool HAS_MASK = MASK != 0;
@@ -592,10 +594,13 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         }
     }
 
-    // Four or more waves (kOnePass) merge and publish in one pass (below);
-    // two merge through LDS records [slot][row][132] (the rings are free
-    // once every wave is past its loop), then wave 0 publishes.
-    constexpr bool kOnePass = WS >= 4;
+    // Four or more waves, and two with short splits (OP), merge and publish
+    // in one pass (kOnePass, below); otherwise the two waves merge through
+    // an LDS record [row][132] (the rings are free once every wave is past
+    // its loop), then wave 0 publishes. (Two waves streaming 1024 cells or
+    // more per split finish further apart, and the one pass, which waits for
+    // both before any store, is then slower.)
+    constexpr bool kOnePass = WS >= 4 || OP;
     if constexpr (WS > 1 && !kOnePass) {
         float * recs = (float *) &lds[0][0][0];
 #pragma unroll
@@ -884,24 +889,48 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     }
 }
 
+template <int WS, int NB, bool OP>
+void launch_masks(const FattnParams & p, const dim3 grid, hipStream_t stream) {
+    const DecodeInputs none = {};
+    if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 2, 1, -1, OP>), grid, dim3(WS * 64), 0, stream, p, none);
+    else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 1, 1, -1, OP>), grid, dim3(WS * 64), 0, stream, p, none);
+    else                      hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, -1, OP>), grid, dim3(WS * 64), 0, stream, p, none);
+}
+
+// p.one_pass selects the one-pass merge for the 2 x 3 shape (the others
+// have it always (four or more waves) or never).
 template <int WS, int NB>
 hipError_t launch_cfg(const FattnParams & p, hipStream_t stream) {
     const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
-    const DecodeInputs none = {};
-    if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 2, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
-    else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 1, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
-    else                      hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, -1>), grid, dim3(WS * 64), 0, stream, p, none);
+    if constexpr (WS == 2 && NB == 3) {
+        if (p.one_pass) {
+            launch_masks<WS, NB, true>(p, grid, stream);
+            return hipGetLastError();
+        }
+    }
+    launch_masks<WS, NB, (WS >= 4)>(p, grid, stream);
     return hipGetLastError();
+}
+
+template <int WS, int NB, bool OP>
+void launch_fused_modes(const FattnParams & p, const DecodeInputs & in, const int mode, hipStream_t stream) {
+    const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, 1);
+    switch (mode) {
+        case 2: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 2, OP>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        case 1: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 1, OP>), grid, dim3(WS * 64), 0, stream, p, in); break;
+        default: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 0, OP>), grid, dim3(WS * 64), 0, stream, p, in); break;
+    }
 }
 
 template <int WS, int NB>
 hipError_t launch_fused(const FattnParams & p, const DecodeInputs & in, const int mode, hipStream_t stream) {
-    const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, 1);
-    switch (mode) {
-        case 2: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 2>), grid, dim3(WS * 64), 0, stream, p, in); break;
-        case 1: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 1>), grid, dim3(WS * 64), 0, stream, p, in); break;
-        default: hipLaunchKernelGGL((fattn_decode_kernel<WS, NB, 0, 1, 0>), grid, dim3(WS * 64), 0, stream, p, in); break;
+    if constexpr (WS == 2) {
+        if (p.one_pass) {
+            launch_fused_modes<WS, NB, true>(p, in, mode, stream);
+            return hipGetLastError();
+        }
     }
+    launch_fused_modes<WS, NB, (WS >= 4)>(p, in, mode, stream);
     return hipGetLastError();
 }
 
@@ -924,9 +953,9 @@ hipError_t fattn_decode_launch(const FattnParams & p, int waves, int stages, hip
         if (p.R > 32 || waves != 8 || stages != 2) return hipErrorInvalidValue;
         const dim3 grid((unsigned) p.n_split, (unsigned) p.Hkv, (unsigned) p.B);
         const DecodeInputs none = {};
-        if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 2, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
-        else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 1, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
-        else                      hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 0, 2, -1>), grid, dim3(8 * 64), 0, stream, p, none);
+        if (p.mask && p.mask_pre) hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 2, 2, -1, true>), grid, dim3(8 * 64), 0, stream, p, none);
+        else if (p.mask)          hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 1, 2, -1, true>), grid, dim3(8 * 64), 0, stream, p, none);
+        else                      hipLaunchKernelGGL((fattn_decode_kernel<8, 2, 0, 2, -1, true>), grid, dim3(8 * 64), 0, stream, p, none);
         return hipGetLastError();
     }
     switch (waves * 10 + stages) {

@@ -40,6 +40,7 @@ struct FattnParams {
     int32_t mask_pre;               // decode kernel: each wave's mask values preloaded into LDS
     int32_t mask_rows;              //   distinct mask rows of a workgroup (32-byte items per stage)
     int32_t mask_wave_bytes;        //   LDS bytes per wave (whole 1 KiB DMA blocks)
+    int32_t one_pass;               // decode kernel, 2 waves: the waves' states merged in one pass
     float *    part;                // split-KV merge records: [units][n_split][rows per tile][record stride]
     unsigned * counters;            // [units] in the fixed counter region, zero between calls
     int *      err;                 // device error flags (al_device_errors): [0, 1] set_rows, [2] a merge gave up waiting

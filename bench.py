@@ -33,7 +33,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 F16_PEAK_TFLOPS = 2500.0       # MI355X dense f16 MFMA, TFLOP/s
-DECODE_KERNEL = "fattn_decode_kernel<2, 3, 0, 1, -1>"   # the launch decode at q_len 1 takes
+DECODE_KERNEL = "fattn_decode_kernel<2, 3, 0, 1, -1, false>"   # the launch decode at q_len 1 takes
 
 
 def parse():

@@ -418,6 +418,59 @@ def test_decode_mask_preloaded_and_per_stage(gpu, monkeypatch):
         assert_parity(a, ref, what=name)
 
 
+def test_decode_two_waves_one_pass_and_tree_merge(gpu, monkeypatch):
+    """The 2-wave decode shape merges its two waves' states in one pass with
+    all threads when a split covers at most AL_DECODE_ONE_PASS_CELLS cells
+    (512 by default), else wave 0 folds in wave 1's state (the tree). Each
+    form against the oracle, and the two against each other (the same two
+    weighted terms, summed in another order: within a few ulp): one token
+    over 4096 and 16384 cells (128 and 512 cells per split), the Qwen3-32B
+    shape (8 rows per kv head), 2-draft verify with the causal mask among
+    the drafts, 2 streams, an explicit mask with holes (preloaded and per
+    stage), and one split over 40 and 10 cells (the pass writes the output
+    rows; a wave with one stage or none)."""
+    rng = np.random.default_rng(91)
+    cases = []
+    for seed, n_kv in ((911, 4096), (912, 16384)):
+        q, k, v = O.make_inputs(seed, T=1, Hq=32, Hkv=8, n_kv=n_kv)
+        cases.append((f"one token over {n_kv} cells", q, k, v, None, dict(kv_len=n_kv)))
+    q, k, v = O.make_inputs(913, T=1, Hq=64, Hkv=8, n_kv=4096)
+    cases.append(("Qwen3-32B shape, 4096 cells", q, k, v, None, dict(kv_len=4096)))
+    q, k, v = O.make_inputs(914, T=2, Hq=32, Hkv=8, n_kv=8192)
+    cases.append(("2 drafts over 8192 cells", q, k, v, None, dict(kv_len=8192, causal_pos0=8190)))
+    q, k, v = O.make_inputs(915, B=2, T=1, Hq=32, Hkv=8, n_kv=3000)
+    cases.append(("2 streams, 3000 cells", q, k, v, None, dict(kv_len=3000)))
+    q, k, v = O.make_inputs(916, T=1, Hq=32, Hkv=8, n_kv=6000)
+    m = np.zeros((1, 1, 64, 6000), np.float16)
+    m[0, 0, 0, rng.choice(6000, 900, replace=False)] = -np.inf
+    m[0, 0, 0, :300] = rng.uniform(-2, 0, 300).astype(np.float16)
+    cases.append(("explicit mask with holes, 6000 cells", q, k, v, m, {}))
+    for seed, n_kv in ((917, 40), (918, 10)):
+        q, k, v = O.make_inputs(seed, T=1, Hq=32, Hkv=8, n_kv=n_kv)
+        cases.append((f"one split over {n_kv} cells", q, k, v, None, dict(kv_len=n_kv)))
+    for name, q, k, v, m, kw in cases:
+        ref = O.attention(q, k, v, m, scale=SCALE, **kw)
+        forms = {}
+        for label, cells, pre in (("one pass", None, None), ("tree", "0", None), ("one pass, mask per stage", None, "0")):
+            if pre is not None and m is None:
+                continue
+            _case(f"{name}: {label}")
+            for var, val in (("AL_DECODE_ONE_PASS_CELLS", cells), ("AL_DECODE_MASK_PRE", pre)):
+                if val is None:
+                    monkeypatch.delenv(var, raising=False)
+                else:
+                    monkeypatch.setenv(var, val)
+            forms[label] = run_gpu(q, k, v, m, scale=SCALE, **kw)
+            assert_parity(forms[label], ref, what=f"{name}: {label}")
+        monkeypatch.delenv("AL_DECODE_ONE_PASS_CELLS", raising=False)
+        monkeypatch.delenv("AL_DECODE_MASK_PRE", raising=False)
+        a, b = forms["one pass"], forms["tree"]
+        assert np.array_equal(np.isnan(a), np.isnan(b)), f"{name}: forms differ in NaN rows"
+        np.testing.assert_allclose(a, b, rtol=2e-6, atol=1e-6, err_msg=f"{name}: one pass against tree")
+        if "one pass, mask per stage" in forms:
+            assert np.array_equal(a, forms["one pass, mask per stage"], equal_nan=True), f"{name}: mask forms differ"
+
+
 def test_verify_waves_without_stages_and_one_pass_merge(gpu):
     """The 8-wave decode shape (17-32 query rows per kv head) merges its
     waves in one pass from their own LDS rings. Short contexts leave some of
