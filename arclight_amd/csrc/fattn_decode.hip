@@ -597,9 +597,8 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
     // Four or more waves, and two with short splits (OP), merge and publish
     // in one pass (kOnePass, below); otherwise the two waves merge through
     // an LDS record [row][132] (the rings are free once every wave is past
-    // its loop), then wave 0 publishes. (Two waves streaming 1024 cells or
-    // more per split finish further apart, and the one pass, which waits for
-    // both before any store, is then slower.)
+    // its loop), then wave 0 publishes. (Measured with two waves: the one
+    // pass is faster up to 512 cells per split, the tree at 1024.)
     constexpr bool kOnePass = WS >= 4 || OP;
     if constexpr (WS > 1 && !kOnePass) {
         float * recs = (float *) &lds[0][0][0];
