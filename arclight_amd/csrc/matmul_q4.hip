@@ -183,21 +183,36 @@ __device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, 
     const float q0 = amax * kR127;
     const float dq = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), kR127, q0);
     const float d = amax <= 3.40282347e+38f ? dq : amax;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    int sum = 0;
+    // id = 1 / d as the IEEE division rounds it: for d in [2^-126, 2^126)
+    // the v_rcp_f32 estimate and one Newton step give exactly that quotient
+    // (checked on gfx950 for every such float); zero, denormal d and the
+    // top two binades take the division
+    float id;
+    if (d >= 0x1p-126f && d < 0x1p126f) {
+        const float r = __builtin_amdgcn_rcpf(d);
+        id = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+    } else {
+        id = d != 0.0f ? 1.0f / d : 0.0f;
+    }
     uint32_t words[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        int q[4];
+        uint32_t y[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            q[k] = (int) rintf(v[4 * j + k] * id);                      // ties to even, as vcvtnq
-            sum += q[k];
+            // rint(v * id), ties to even as vcvtnq: the product (|p| <= 127)
+            // plus 1.5 * 2^23 rounds to the integer k + 1.5 * 2^23, whose
+            // float holds k in its low bits (two's complement in the low byte);
+            // the product is kept out of a fused multiply-add
+            float pr = v[4 * j + k] * id;
+            asm volatile("" : "+v"(pr));
+            y[k] = __float_as_uint(pr + 12582912.0f);
         }
-        // the four low bytes into one word (v_perm: bytes of q0, q1 | of q2, q3)
-        words[j] = __builtin_amdgcn_perm((uint32_t) q[1], (uint32_t) q[0], 0x0c0c0400u) |
-                   __builtin_amdgcn_perm((uint32_t) q[3], (uint32_t) q[2], 0x04000c0cu);
+        // the four low bytes into one word (v_perm: bytes of y0, y1 | of y2, y3)
+        words[j] = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u) | __builtin_amdgcn_perm(y[3], y[2], 0x04000c0cu);
     }
+    // the eight values' sum: the signed bytes dotted with ones
+    const int sum = __builtin_amdgcn_sdot4((int) words[1], 0x01010101, __builtin_amdgcn_sdot4((int) words[0], 0x01010101, 0, false), false);
     float fs = (float) sum;                                             // |sum| <= 1016: exact in f32
     fs += dpp<kQuadXor1>(fs);
     fs += dpp<kQuadXor2>(fs);
