@@ -82,6 +82,7 @@ SIGNATURES = {
     "al_fattn_f16_with_inputs": (_I, [ctypes.POINTER(abi.AlAttnInputsArgs), ctypes.POINTER(abi.AlFattnArgs)]),
     # include/arclight_matmul.h
     "al_mul_mat_q4_0_f32": (_I, [ctypes.POINTER(abi.AlTensor)] * 3 + [_VP]),
+    "al_mul_mat_q4_0_check_inverse": (_I, [ctypes.POINTER(ctypes.c_ulonglong)]),
 }
 
 _lib = None

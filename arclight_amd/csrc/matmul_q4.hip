@@ -165,6 +165,33 @@ __global__ __launch_bounds__(256) void gemv_q4_kernel(const char * __restrict__ 
     }
 }
 
+// 1 / d as the IEEE division rounds it, for a Q8_0 block scale d >= 0 (0
+// for d = 0, as quantize_row_q8_0 takes it): for d in [2^-126, 2^126) the
+// v_rcp_f32 estimate and one Newton step give that quotient
+// (al_mul_mat_q4_0_check_inverse counts the floats where they do not);
+// zero, denormal d and the top two binades take the division.
+__device__ __forceinline__ float q8_inverse(const float d) {
+    if (d >= 0x1p-126f && d < 0x1p126f) {
+        const float r = __builtin_amdgcn_rcpf(d);
+        return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+    }
+    return d != 0.0f ? 1.0f / d : 0.0f;
+}
+
+// Every non-negative float bit pattern up to +inf (grid-stride): counts the
+// ones where q8_inverse differs from the division, bit for bit.
+__global__ __launch_bounds__(256) void q8_inverse_check_kernel(unsigned long long * bad) {
+    unsigned long long n = 0;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t u = blockIdx.x * blockDim.x + threadIdx.x; u <= 0x7f800000u; u += stride) {
+        const float d = __uint_as_float(u);
+        const float ref = d != 0.0f ? 1.0f / d : 0.0f;
+        n += __float_as_uint(q8_inverse(d)) != __float_as_uint(ref);
+        if (u > 0x7f800000u - stride) break;
+    }
+    if (n) atomicAdd(bad, n);
+}
+
 // Eight values of a Q8_0 block (part 0..3 of it, the four parts in the four
 // lanes of a quad) quantized into LDS.
 __device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, const int part, int8_t * qdst,
@@ -183,17 +210,7 @@ __device__ __forceinline__ void quantize_part(const float4 f0, const float4 f1, 
     const float q0 = amax * kR127;
     const float dq = __builtin_fmaf(__builtin_fmaf(-q0, 127.0f, amax), kR127, q0);
     const float d = amax <= 3.40282347e+38f ? dq : amax;
-    // id = 1 / d as the IEEE division rounds it: for d in [2^-126, 2^126)
-    // the v_rcp_f32 estimate and one Newton step give exactly that quotient
-    // (checked on gfx950 for every such float); zero, denormal d and the
-    // top two binades take the division
-    float id;
-    if (d >= 0x1p-126f && d < 0x1p126f) {
-        const float r = __builtin_amdgcn_rcpf(d);
-        id = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
-    } else {
-        id = d != 0.0f ? 1.0f / d : 0.0f;
-    }
+    const float id = q8_inverse(d);
     uint32_t words[2];
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -434,6 +451,23 @@ int scratch(size_t bytes, void ** out) {
 }
 
 }  // namespace
+
+extern "C" int al_mul_mat_q4_0_check_inverse(unsigned long long * mismatches) {
+    if (!mismatches) return al_fail(AL_ERR_INVALID, "al_mul_mat_q4_0_check_inverse: mismatches required");
+    unsigned long long * dev = nullptr;
+    hipError_t e = hipMalloc(&dev, sizeof(unsigned long long));
+    if (e != hipSuccess) return al_hip_fail(e, "check_inverse: hipMalloc");
+    e = hipMemset(dev, 0, sizeof(unsigned long long));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(q8_inverse_check_kernel, dim3(4096), dim3(256), 0, (hipStream_t) 0, dev);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(mismatches, dev, sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    const hipError_t f = hipFree(dev);
+    if (e != hipSuccess) return al_hip_fail(e, "check_inverse");
+    if (f != hipSuccess) return al_hip_fail(f, "check_inverse: hipFree");
+    return AL_OK;
+}
 
 extern "C" int al_mul_mat_q4_0_f32(const al_tensor * w, const al_tensor * x, const al_tensor * y, void * stream) {
     if (!w || !x || !y || !w->data || !x->data || !y->data) return al_fail(AL_ERR_INVALID, "mul_mat_q4_0: w, x and y required");

@@ -47,3 +47,12 @@ def mul_mat_q4_0(w, x, y=None, stream=None):
     call("al_mul_mat_q4_0_f32", ctypes.byref(wd), ctypes.byref(xd), ctypes.byref(yd),
          stream.handle if stream is not None else None)
     return y
+
+
+def check_inverse():
+    """Floats d in [0, +inf] where the Q8_0 quantization's reciprocal of a
+    block scale (hardware estimate and one Newton step on [2^-126, 2^126))
+    differs from the IEEE quotient 1 / d: 0 on a correct device."""
+    n = ctypes.c_ulonglong(0)
+    call("al_mul_mat_q4_0_check_inverse", ctypes.byref(n))
+    return n.value

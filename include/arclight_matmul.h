@@ -39,6 +39,16 @@ extern "C" {
  */
 int al_mul_mat_q4_0_f32(const al_tensor * w, const al_tensor * x, const al_tensor * y, void * stream);
 
+/*
+ * No counterpart in the reference: a self-check of the device for callers
+ * that want to confirm its arithmetic. The Q8_0 quantization above takes
+ * 1 / d of a block scale d in [2^-126, 2^126) from the hardware reciprocal
+ * estimate and one Newton step instead of a division; this counts, over
+ * every non-negative float up to +inf, the values where that differs from
+ * the IEEE quotient (0 on gfx950). Synchronous, on the default stream.
+ */
+int al_mul_mat_q4_0_check_inverse(unsigned long long * mismatches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -129,3 +129,12 @@ def test_wo_rejects_mismatched_operands(gpu):
     with pytest.raises(_lib.ArclightError) as e:
         matmul.mul_mat_q4_0(wm, xh)
     assert e.value.status == abi.AL_ERR_UNSUPPORTED
+
+
+def test_q8_scale_inverse_equals_division(gpu):
+    """The quantization's 1 / d (v_rcp_f32 and one Newton step for d in
+    [2^-126, 2^126), the division elsewhere) equals the IEEE quotient for
+    every non-negative float up to +inf, bit for bit."""
+    from arclight_amd import matmul
+    _case("Q8_0 scale inverse over every float")
+    assert matmul.check_inverse() == 0
