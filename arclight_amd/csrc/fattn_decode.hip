@@ -466,12 +466,9 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                         *(const u32x4 *) (kv16 + part * 256 + gj * 16);
                 }
             }
-            u32x4 kf[4];
-#pragma unroll
-            for (int kb = 0; kb < 4; ++kb) kf[kb] = *(const u32x4 *) (st + kread + (((4 * kb + g) ^ n) << 4));
-            half4 vt[8];
-#pragma unroll
-            for (int mb = 0; mb < 8; ++mb) vt[mb] = lds_read_tr16(st + vread + (((2 * mb + ((n & 3) >> 1)) ^ vcell) << 4));
+            // the mask values first: LDS reads complete in order, so the
+            // stage's mask test then waits for them alone, not for the K and
+            // V^T operands behind them
             uint2 mk[RB];
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
@@ -479,6 +476,12 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
                 if constexpr (MASK == 1) mk[rb] = *(const uint2 *) (st + 8192 + 32 * (16 * rb + n) + 8 * g);
                 if constexpr (MASK == 2) mk[rb] = *(const uint2 *) (mp[rb] + j * 32 * p.mask_rows);
             }
+            u32x4 kf[4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) kf[kb] = *(const u32x4 *) (st + kread + (((4 * kb + g) ^ n) << 4));
+            half4 vt[8];
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) vt[mb] = lds_read_tr16(st + vread + (((2 * mb + ((n & 3) >> 1)) ^ vcell) << 4));
 
             // a stage is taken whole when the length / causal limit passes it
             // and, with a mask, every mask value of the stage is +0 (the
