@@ -471,6 +471,33 @@ def test_decode_two_waves_one_pass_and_tree_merge(gpu, monkeypatch):
             assert np.array_equal(a, forms["one pass, mask per stage"], equal_nan=True), f"{name}: mask forms differ"
 
 
+def test_decode_two_waves_sinks_softcap_alibi_both_merges(gpu, monkeypatch):
+    """One token per stream (the 2-wave shape) with attention sinks, logit
+    softcap and ALiBi over a mask with finite biases, against the oracle,
+    with the one-pass and the tree merge of the waves: 4096 cells (128 per
+    split: one pass by default) and 20000 cells (640 per split: the tree),
+    each also with the other form forced."""
+    rng = np.random.default_rng(93)
+    for seed, n_kv in ((931, 4096), (932, 20000)):
+        q, k, v = O.make_inputs(seed, T=1, Hq=32, Hkv=8, n_kv=n_kv)
+        sinks = rng.standard_normal(32).astype(np.float32) * 3
+        m = np.zeros((1, 1, 64, n_kv), np.float16)
+        m[0, 0, 0, :] = (-np.arange(n_kv, dtype=np.float32)[::-1] / 4096.0).astype(np.float16)
+        m[0, 0, 0, rng.choice(n_kv, n_kv // 10, replace=False)] = -np.inf
+        for cells in (None, "0", "100000"):
+            label = {None: "default", "0": "tree", "100000": "one pass"}[cells]
+            if cells is None:
+                monkeypatch.delenv("AL_DECODE_ONE_PASS_CELLS", raising=False)
+            else:
+                monkeypatch.setenv("AL_DECODE_ONE_PASS_CELLS", cells)
+            _case(f"{n_kv} cells, sinks: {label}")
+            _check(f"{n_kv} cells, sinks ({label})", q, k, v, m, sinks, scale=SCALE)
+            _case(f"{n_kv} cells, softcap + ALiBi: {label}")
+            _check(f"{n_kv} cells, softcap + ALiBi ({label})", q, k, v, m, scale=SCALE * 4, logit_softcap=5.0,
+                   max_bias=8.0)
+        monkeypatch.delenv("AL_DECODE_ONE_PASS_CELLS", raising=False)
+
+
 def test_verify_waves_without_stages_and_one_pass_merge(gpu):
     """The 8-wave decode shape (17-32 query rows per kv head) merges its
     waves in one pass from their own LDS rings. Short contexts leave some of
