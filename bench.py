@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip the 4K/16K decode, 8K verify and Qwen3-32B-shape lines")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="target CPU-baseline sample time")
-    ap.add_argument("--only", choices=["decode", "prefill", "wo", "copy", "step"], default=None,
+    ap.add_argument("--only", choices=["decode", "decode_mask", "prefill", "wo", "copy", "step"], default=None,
                     help="run one workload only (for profiling); prints its own JSON line")
     return ap.parse_args()
 
@@ -502,6 +502,9 @@ def main():
                                  for K, N, T, c in [(4096, 2560, 1, 64), (4096, 2560, 8, 64), (8192, 5120, 1, 16)]]}))
         return
 
+    if a.only == "decode_mask":
+        print(json.dumps({"decode_explicit_mask": bench_decode(lib, stream, a, explicit_mask=True)}))
+        return
     dec = bench_decode(lib, stream, a)
     print(f"[bench] decode {dec}", file=sys.stderr, flush=True)
     if a.only == "decode":
