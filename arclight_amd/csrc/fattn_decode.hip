@@ -189,11 +189,12 @@ __global__ __launch_bounds__(WS * 64) void fattn_decode_kernel(const FattnParams
         const uint32_t cs = (uint32_t) (wbase + wstride * j);
         const uint32_t kofs = cs * k_nb1 + dk, vofs = cs * v_nb1 + dv;
         const uint32_t base = ring + (uint32_t) (u * STAGE);
+        // the stage's V rows, then its K rows (grouped by tensor: 0.3-0.4 µs
+        // per launch faster at 32K than K and V alternating, measured)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            dma16(kd, kofs + (uint32_t) (4 * i) * k_nb1 + dj[i], base + (uint32_t) (i * 1024));
-            dma16(vd, vofs + (uint32_t) (4 * i) * v_nb1 + dj[i], base + (uint32_t) (4096 + i * 1024));
-        }
+        for (int i = 0; i < 4; ++i) dma16(vd, vofs + (uint32_t) (4 * i) * v_nb1 + dj[i], base + (uint32_t) (4096 + i * 1024));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) dma16(kd, kofs + (uint32_t) (4 * i) * k_nb1 + dj[i], base + (uint32_t) (i * 1024));
         if constexpr (MASK == 1) dma16(md, msrc + cs * 2, base + 8192u);
     };
 
